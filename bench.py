@@ -1,0 +1,271 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X low-bit projection path (one JSON line on stdout).
+
+Headline (``value``): the Marlin-layout W4A16 decode GEMV of BASELINE.json
+configs[1] at M=1 -- K=5120, N=17408, group 128 -- in GB/s of algorithmic
+bytes (K*N/2 + (K/128)*N*2 + M*K*2 + M*N*2 per call).  A "step" is one call.
+Inputs are resident in HBM before timing; the call sequence cycles through
+``--sets`` independent weight sets (>256 MB in total, so the 256 MB Infinity
+Cache cannot serve the weights) and is replayed from a HIP graph so the
+timed region measures back-to-back kernels, not Python launch overhead.
+
+Extra fields report the other BASELINE configs: M=4/16 decode, the M=2048
+prefill GEMM in TFLOP/s (both shapes), the rowwise fallback sweep, and the
+64-layer decode-step projection sweep.  ``cpu_baseline`` times the CPU
+restatement of the reference's dequantise-then-matmul path on a bounded
+sample of the headline workload.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor spec
+FP16_DENSE_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 flop/clk, vendor spec
+MALL_BYTES = 256 * 1024 * 1024
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def marlin_bytes(m, k, n, g=128):
+    groups = 1 if g <= 0 else k // g
+    return k * n // 2 + groups * n * 2 + m * k * 2 + m * n * 2
+
+
+def rowwise_bytes(m, k, n, bits, g):
+    return n * ((k * bits + 7) // 8) + n * math.ceil(k / g) * 2 + m * k * 2 + m * n * 2
+
+
+class MarlinProblem:
+    """`sets` independent random Marlin weight sets of one shape (codes uniform in [0,16))."""
+
+    def __init__(self, torch, dev, m, k, n, sets, seed):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        self.m, self.k, self.n = m, k, n
+        self.q = [torch.randint(-2 ** 31, 2 ** 31, (k // 16, 2 * n), dtype=torch.int32, device=dev, generator=gen)
+                  for _ in range(sets)]
+        self.s = [(torch.randn((k // 128, n), device=dev, generator=gen) * 0.01).abs_().add_(1e-3).half()
+                  for _ in range(sets)]
+        self.x = torch.randn((m, k), device=dev, generator=gen).half()
+        self.out = [torch.empty((m, n), dtype=torch.float16, device=dev) for _ in range(sets)]
+        self.ws = torch.zeros((n // 128 * 16,), dtype=torch.int32, device=dev)
+
+    def call(self, lc, i):
+        lc.lowbit_marlin_gemm_out(self.q[i], self.s[i], self.x, self.out[i], self.ws, self.k, 128)
+
+
+class RowwiseProblem:
+    def __init__(self, torch, dev, k, n, bits, g, sets, seed):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        self.k, self.n, self.bits, self.g = k, n, bits, g
+        pc = (k * bits + 7) // 8
+        self.q = [torch.randint(0, 256, (n, pc), dtype=torch.uint8, device=dev, generator=gen) for _ in range(sets)]
+        self.s = [(torch.randn((n, math.ceil(k / g)), device=dev, generator=gen) * 0.01).abs_().add_(1e-3).half()
+                  for _ in range(sets)]
+        self.x = torch.randn((k,), device=dev, generator=gen).half()
+
+    def call(self, lc, i):
+        lc.lowbit_gemv(self.q[i], self.s[i], self.x, self.k, self.g, self.bits)
+
+
+def time_calls(torch, fn, n_sets, steps, warmup, use_graph=True):
+    """Runs `steps` calls cycling over `n_sets` sets; returns (elapsed_ms, steps_done).
+
+    With use_graph the calls of one cycle are captured once in a HIP graph and
+    replayed; events bracket the replays on the launch stream."""
+    rounds = max(1, steps // n_sets)
+    warm_rounds = max(1, warmup // n_sets)
+    stream = torch.cuda.current_stream()
+    if use_graph:
+        side = torch.cuda.Stream()
+        side.wait_stream(stream)
+        with torch.cuda.stream(side):
+            for i in range(n_sets):  # eager warm-up before capture
+                fn(i)
+        stream.wait_stream(side)
+        torch.cuda.synchronize()
+        graph = torch.cuda.CUDAGraph()
+        with torch.cuda.graph(graph):
+            for i in range(n_sets):
+                fn(i)
+        run_round = graph.replay
+    else:
+        def run_round():
+            for i in range(n_sets):
+                fn(i)
+    for _ in range(warm_rounds):
+        run_round()
+    torch.cuda.synchronize()
+    start = torch.cuda.Event(enable_timing=True)
+    stop = torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(rounds):
+        run_round()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    return start.elapsed_time(stop), rounds * n_sets
+
+
+def sets_for(bytes_per_set, minimum=8):
+    return max(minimum, math.ceil(2.0 * MALL_BYTES / bytes_per_set))
+
+
+def cpu_baseline(m, k, n):
+    """CPU restatement of the dequantise-then-matmul reference path on the headline
+    shape (oracle package; the reference raises for Marlin on CPU, ops.py:65-79)."""
+    import numpy as np
+    from threadpoolctl import threadpool_info
+
+    from oracle import lowbit_oracle as O
+
+    rng = np.random.default_rng(0)
+    qw = rng.integers(-2 ** 31, 2 ** 31, size=(k // 16, 2 * n), dtype=np.int64).astype(np.int32)
+    s = (np.abs(rng.normal(0, 0.01, (k // 128, n))) + 1e-3).astype(np.float16)
+    x = rng.normal(0, 1, (m, k)).astype(np.float16)
+    O.marlin_gemm(x, qw, s, 128)  # warm-up
+    times = []
+    t_end = time.perf_counter() + 15.0
+    while len(times) < 3 and (not times or time.perf_counter() < t_end):
+        t0 = time.perf_counter()
+        O.marlin_gemm(x, qw, s, 128)
+        times.append(time.perf_counter() - t0)
+    sec = sum(times) / len(times)
+    threads = max([t.get("num_threads", 1) for t in threadpool_info()] + [1])
+    return {
+        "value": round(marlin_bytes(m, k, n) / sec / 1e9, 4),
+        "unit": "GB/s",
+        "cores": int(threads),
+        "kind": "port",
+        "sample": f"{len(times)} full calls of M={m} K={k} N={n} g128 (numpy unpack + fp16 dequant single-threaded, "
+                  f"float64 matmul on {threads} BLAS threads); {sec * 1e3:.0f} ms/call",
+        "cpu": platform.processor() or platform.machine(),
+    }
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=3000)
+    ap.add_argument("--warmup", type=int, default=300)
+    ap.add_argument("--sets", type=int, default=0, help="weight sets to rotate (0 = enough to exceed 2x MALL)")
+    ap.add_argument("--no-graph", action="store_true")
+    ap.add_argument("--skip-cpu", action="store_true")
+    ap.add_argument("--skip-extra", action="store_true")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+
+    import neurova_amd  # noqa: F401  (registers langburst_cuda)
+    import langburst_cuda as lc
+
+    if not torch.cuda.is_available():
+        print("bench.py needs a GPU", file=sys.stderr)
+        sys.exit(1)
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    use_graph = not args.no_graph
+    log(f"[bench] device {torch.cuda.get_device_name(dev)}; graph={use_graph}")
+
+    # ---- headline: Marlin decode GEMV, M=1 ----
+    m, k, n = 1, 5120, 17408
+    per_call = marlin_bytes(m, k, n)
+    n_sets = args.sets or sets_for(per_call)
+    prob = MarlinProblem(torch, dev, m, k, n, n_sets, seed=1)
+    log(f"[bench] headline M={m} K={k} N={n}: {n_sets} weight sets ({n_sets * per_call / 2**20:.0f} MiB)")
+    torch.cuda.synchronize()
+    ms, steps = time_calls(torch, lambda i: prob.call(lc, i), n_sets, args.steps, args.warmup, use_graph)
+    us_per = ms * 1e3 / steps
+    gbs = per_call / (us_per * 1e-6) / 1e9
+    log(f"[bench] headline {us_per:.2f} us/call, {gbs:.1f} GB/s")
+    del prob
+    torch.cuda.empty_cache()
+
+    result = {
+        "metric": "W4A16 GEMV GB/s (M=1) & GEMM TFLOP/s (M=2048), % of MI355X roofline",
+        "value": round(gbs, 2),
+        "unit": "GB/s",
+        "n_gpus": 1,
+        "steps": steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms / steps, 6),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp16 (int4 weights, fp32 accumulate)",
+        "data": "synthetic (uniform int4 codes, |N(0,0.01)|+1e-3 fp16 scales, N(0,1) fp16 activations)",
+        "config": {"workload": f"marlin_w4a16_gemv M=1 K=5120 N=17408 g128, {n_sets} rotating weight sets"
+                               + (", hipGraph replay" if use_graph else ", eager launches"),
+                   "m": m, "k": k, "n": n, "group_size": 128, "weight_sets": n_sets},
+        "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "bytes_per_launch": per_call, "us_per_launch": round(us_per, 3)},
+    }
+
+    if not args.skip_extra:
+        extra = {}
+        for mm in (4, 16):
+            pc = marlin_bytes(mm, k, n)
+            ns = sets_for(pc)
+            pr = MarlinProblem(torch, dev, mm, k, n, ns, seed=2 + mm)
+            ms2, st2 = time_calls(torch, lambda i: pr.call(lc, i), ns, 600, 60, use_graph)
+            u = ms2 * 1e3 / st2
+            extra[f"marlin_gemv_m{mm}"] = {"us_per_call": round(u, 3), "GB/s": round(pc / u / 1e3, 1),
+                                           "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4)}
+            log(f"[bench] M={mm}: {u:.2f} us, {pc / u / 1e3:.1f} GB/s")
+            del pr
+        for (kk, nn) in ((5120, 17408), (17408, 5120)):
+            mm = 2048
+            pr = MarlinProblem(torch, dev, mm, kk, nn, 2, seed=11)
+            ms2, st2 = time_calls(torch, lambda i: pr.call(lc, i), 2, 20, 4, use_graph)
+            u = ms2 * 1e3 / st2
+            tf = 2.0 * mm * kk * nn / (u * 1e-6) / 1e12
+            extra[f"marlin_gemm_m2048_k{kk}_n{nn}"] = {"us_per_call": round(u, 2), "TFLOP/s": round(tf, 1),
+                                                       "frac_fp16_peak": round(tf / FP16_DENSE_PEAK_TFLOPS, 4)}
+            log(f"[bench] GEMM M=2048 K={kk} N={nn}: {u:.1f} us, {tf:.1f} TFLOP/s")
+            del pr
+        for bits in (2, 3, 8):
+            for g in (64, 128):
+                pc = rowwise_bytes(1, 17408, 5120, bits, g)
+                ns = sets_for(pc)
+                pr = RowwiseProblem(torch, dev, 17408, 5120, bits, g, ns, seed=bits * g)
+                ms2, st2 = time_calls(torch, lambda i: pr.call(lc, i), ns, 400, 40, use_graph)
+                u = ms2 * 1e3 / st2
+                extra[f"rowwise_b{bits}_g{g}"] = {"us_per_call": round(u, 3), "GB/s": round(pc / u / 1e3, 1),
+                                                  "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4)}
+                log(f"[bench] rowwise b{bits} g{g}: {u:.2f} us, {pc / u / 1e3:.1f} GB/s")
+                del pr
+        pc = rowwise_bytes(1, 4096, 4096, 4, 128)
+        ns = sets_for(pc)
+        pr = RowwiseProblem(torch, dev, 4096, 4096, 4, 128, ns, seed=5)
+        ms2, st2 = time_calls(torch, lambda i: pr.call(lc, i), ns, 400, 40, use_graph)
+        u = ms2 * 1e3 / st2
+        extra["rowwise_cfg1_b4_4096"] = {"us_per_call": round(u, 3), "GB/s": round(pc / u / 1e3, 1),
+                                         "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4)}
+        del pr
+        torch.cuda.empty_cache()
+        result["extra"] = extra
+
+    if not args.skip_cpu:
+        try:
+            result["cpu_baseline"] = cpu_baseline(m, k, n)
+        except Exception as exc:  # the baseline is reported, never required
+            result["cpu_baseline"] = {"value": None, "unit": "GB/s", "cores": 0, "kind": "port",
+                                      "sample": f"failed: {exc}"}
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

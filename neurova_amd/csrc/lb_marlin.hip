@@ -1,0 +1,417 @@
+// Host dispatch and C-ABI entry points for the Marlin-layout W4A16 path:
+// GEMM (decode and prefill kernels), SiLU-gated A prologue, fused argmax,
+// dense dequant and the streaming MLP.
+
+#include <stdlib.h>
+
+#include "marlin_gemm.hpp"
+#include "marlin_skinny.hpp"
+
+namespace lb {
+namespace marlin {
+
+// ---------------------------------------------------------------------------
+// Dense dequant W[N, K] (test / utility path).  Closed-form position of
+// weight (k, n) in the Marlin layout: row kb = k>>4, chunk n>>6, slot
+// 4c+q (c = n&7, q = (k&7)>>1), word j = (n&63)>>4, nibble
+// 4*(k&1) + 2*((n>>3)&1) + (k>>3 & 1).
+// ---------------------------------------------------------------------------
+__device__ __forceinline__ uint32_t code_at(const uint32_t* b, int64_t n_total, int64_t k, int64_t n) {
+  const int64_t kb = k >> 4;
+  const int ki = (int)(k & 15);
+  const int nn = (int)(n & 63);
+  const int j = nn >> 4, c = nn & 7, h = (nn >> 3) & 1;
+  const int q = (ki & 7) >> 1;
+  const int nib = 4 * (ki & 1) + 2 * h + (ki >> 3);
+  const uint32_t w = b[kb * 2 * n_total + (n >> 6) * 128 + (4 * c + q) * 4 + j];
+  return (w >> (4 * nib)) & 15u;
+}
+
+__device__ __forceinline__ uint16_t scale_at(const uint16_t* s, int64_t n_total, int64_t grp, int64_t n, int grouped) {
+  if (grouped) {
+    const int nn = (int)(n & 63);
+    return s[grp * n_total + (n >> 6) * 64 + 8 * (nn & 7) + (nn >> 3)];
+  }
+  const int r = (int)(n & 31);
+  return s[(n & ~31LL) + 8 * ((r >> 1) & 3) + ((r >> 3) << 1) + (r & 1)];
+}
+
+__global__ void dequant_kernel(const uint32_t* __restrict__ b, const uint16_t* __restrict__ s, uint16_t* __restrict__ w,
+                               int64_t n_total, int64_t k_total, int grouped) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= n_total * k_total) return;
+  const int64_t n = idx / k_total;
+  const int64_t k = idx - n * k_total;
+  const f16 q = (f16)((int)code_at(b, n_total, k, n) - 8);
+  f16 v = q;
+  if (grouped) v = q * __builtin_bit_cast(f16, scale_at(s, n_total, k >> 7, n, 1));
+  w[idx] = __builtin_bit_cast(uint16_t, v);
+}
+
+// ---------------------------------------------------------------------------
+// Streaming-MLP numerics (float32 weights (q-8)*s, float32 activations).
+// One wave per (64-column chunk, k split); each lane reads its natural
+// 16-byte slot (fully coalesced) and keeps 8 column sums per batch row.
+// ---------------------------------------------------------------------------
+constexpr int kF32Batch = 4;
+
+template <bool XF32>
+__global__ __launch_bounds__(64) void f32_gemv_kernel(const uint32_t* __restrict__ b, const uint16_t* __restrict__ s,
+                                                      const void* __restrict__ xin, float* __restrict__ partial,
+                                                      int m_total, int64_t n_total, int64_t k_total, int grouped,
+                                                      int splits) {
+  const int lane = threadIdx.x;
+  const int64_t chunk = blockIdx.x;
+  const int split = blockIdx.y;
+  const int m0 = blockIdx.z * kF32Batch;
+  const int pr = lane >> 5, slot = lane & 31, c = slot >> 2, q = slot & 3;
+  const int64_t kp_total = k_total >> 5;
+  const int64_t kp0 = kp_total * split / splits, kp1 = kp_total * (split + 1) / splits;
+  float acc[kF32Batch][4][2];
+#pragma unroll
+  for (int mm = 0; mm < kF32Batch; ++mm)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[mm][j][0] = acc[mm][j][1] = 0.f;
+  for (int64_t kp = kp0; kp < kp1; ++kp) {
+    const int64_t kb = 2 * kp + pr;
+    const u32x4 w = *reinterpret_cast<const u32x4*>(b + kb * 2 * n_total + chunk * 128 + slot * 4);
+    const int64_t kbase = kb * 16 + 2 * q;  // k offsets {0, 1, 8, 9}
+    float xv[kF32Batch][4];
+#pragma unroll
+    for (int mm = 0; mm < kF32Batch; ++mm) {
+      const int m = min(m0 + mm, m_total - 1);
+      const int64_t off = (int64_t)m * k_total + kbase;
+      if (XF32) {
+        const float* x = reinterpret_cast<const float*>(xin);
+        xv[mm][0] = x[off]; xv[mm][1] = x[off + 1]; xv[mm][2] = x[off + 8]; xv[mm][3] = x[off + 9];
+      } else {
+        const uint16_t* x = reinterpret_cast<const uint16_t*>(xin);
+        xv[mm][0] = h2f(x[off]); xv[mm][1] = h2f(x[off + 1]); xv[mm][2] = h2f(x[off + 8]); xv[mm][3] = h2f(x[off + 9]);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t word = w[j];
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        const int64_t n = chunk * 64 + 16 * j + 8 * h + c;
+        const float sc = h2f(scale_at(s, n_total, grouped ? (kb * 16) >> 7 : 0, n, grouped));
+        // nibbles for column c+8h: k offsets 0 (nib 2h), 8 (nib 2h+1), 1 (nib 4+2h), 9 (nib 5+2h)
+        const float w0 = (float)((int)((word >> (8 * h)) & 15u) - 8) * sc;
+        const float w8 = (float)((int)((word >> (8 * h + 4)) & 15u) - 8) * sc;
+        const float w1 = (float)((int)((word >> (16 + 8 * h)) & 15u) - 8) * sc;
+        const float w9 = (float)((int)((word >> (20 + 8 * h)) & 15u) - 8) * sc;
+#pragma unroll
+        for (int mm = 0; mm < kF32Batch; ++mm)
+          acc[mm][j][h] += w0 * xv[mm][0] + w1 * xv[mm][1] + w8 * xv[mm][2] + w9 * xv[mm][3];
+      }
+    }
+  }
+#pragma unroll
+  for (int mm = 0; mm < kF32Batch; ++mm)
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int h = 0; h < 2; ++h) {
+        float v = quad_sum(acc[mm][j][h]);
+        v += __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, v)));
+        if (lane < 32 && q == 0 && m0 + mm < m_total)
+          partial[((int64_t)split * m_total + m0 + mm) * n_total + chunk * 64 + 16 * j + 8 * h + c] = v;
+      }
+}
+
+__global__ void mlp_act_kernel(const float* __restrict__ gu, float* __restrict__ act, int m_total, int64_t inter,
+                               int splits) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= (int64_t)m_total * inter) return;
+  const int64_t m = idx / inter, i = idx - m * inter;
+  float g = 0.f, u = 0.f;
+  for (int sp = 0; sp < splits; ++sp) {
+    const float* row = gu + ((int64_t)sp * m_total + m) * 2 * inter;
+    g += row[i];
+    u += row[inter + i];
+  }
+  act[idx] = (g / (1.0f + __expf(-g))) * u;
+}
+
+__global__ void f32_finalize_kernel(const float* __restrict__ partial, uint16_t* __restrict__ out, int64_t count,
+                                    int splits) {
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= count) return;
+  float v = 0.f;
+  for (int sp = 0; sp < splits; ++sp) v += partial[(int64_t)sp * count + idx];
+  out[idx] = f2h(v);
+}
+
+// ---------------------------------------------------------------------------
+// Planning
+// ---------------------------------------------------------------------------
+constexpr size_t kAlign = 256;
+inline size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
+
+struct Plan {
+  bool skinny = true;
+  int mb = 1;        // GEMM: 16-row blocks per workgroup
+  int n_mb = 1;
+  int n_cg = 0;
+  int splits = 1;
+  size_t lds = 0;    // decode kernel dynamic LDS
+  size_t partial_bytes = 0;
+  size_t keys_bytes = 0;
+};
+
+constexpr int kSkinnyTargetWGs = 512;  // 2048 waves: ~8 per CU
+constexpr int kGemmTargetWGs = 512;    // two workgroups per CU
+constexpr size_t kSkinnyMaxX = 48 * 1024;
+
+inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
+  Plan pl;
+  pl.n_cg = (int)(n / 256);
+  const int groups = (int)(k / 128);
+  if (m <= skinny::kMaxM) {
+    pl.skinny = true;
+    int s = (kSkinnyTargetWGs + pl.n_cg - 1) / pl.n_cg;
+    const size_t x_all = (size_t)k * (size_t)m * 2;
+    const int s_lds = (int)((x_all + kSkinnyMaxX - 1) / kSkinnyMaxX);
+    if (s < s_lds) s = s_lds;
+    if (s > groups) s = groups;
+    if (s < 1) s = 1;
+    if (s > 1 && workspace_len < (int64_t)pl.n_cg + 1) s = 1;
+    pl.splits = s;
+    const int max_groups = (groups + s - 1) / s;
+    pl.lds = (size_t)max_groups * 128 * (size_t)m * 2 + skinny::kWaves * 64 * 16;
+  } else {
+    pl.skinny = false;
+    pl.mb = m > 64 ? 8 : (m > 32 ? 4 : 2);
+    const int64_t bm = 16 * pl.mb;
+    pl.n_mb = (int)((m + bm - 1) / bm);
+    const int64_t tiles = (int64_t)pl.n_cg * pl.n_mb;
+    int s = 1;
+    if (tiles < kGemmTargetWGs) s = (int)((kGemmTargetWGs + tiles - 1) / tiles);
+    if (s > groups) s = groups;
+    if (s < 1) s = 1;
+    if (s > 1 && workspace_len < tiles + 1) s = 1;
+    pl.splits = s;
+  }
+  pl.partial_bytes = pl.splits > 1 ? align_up((size_t)pl.splits * (size_t)m * (size_t)n * 4) : 0;
+  pl.keys_bytes = align_up((size_t)m * (size_t)pl.n_cg * 8);
+  return pl;
+}
+
+// Workspace entries a launch uses: [0] the argmax arrival counter, [1 + tile]
+// the split-K counters of each output tile.
+inline int64_t counters_needed(const Plan& pl, bool argmax) {
+  if (pl.splits > 1) return 1 + (int64_t)pl.n_cg * pl.n_mb;
+  return argmax ? 1 : 0;
+}
+
+inline int normalize_group(int64_t g, int64_t k, int& grouped) {
+  if (g <= 0 || g == k) {
+    grouped = 0;
+    return LB_OK;
+  }
+  if (g == 128) {
+    grouped = 1;
+    return LB_OK;
+  }
+  return LB_ERR_PROB_SHAPE;
+}
+
+enum Variant { V_PLAIN = 0, V_SILU = 1, V_ARGMAX = 2 };
+
+int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uint16_t* s, int64_t m, int64_t n,
+        int64_t k, int32_t* workspace, int64_t workspace_len, int64_t groupsize, int64_t* argmax_state,
+        int64_t* argmax_out, void* scratch, size_t scratch_bytes, hipStream_t st) {
+  if (m < 0 || n < 0 || k < 0) return LB_ERR_ARG;
+  if (n % 256 != 0 || k % 128 != 0) return LB_ERR_PROB_SHAPE;
+  int grouped = 0;
+  if (normalize_group(groupsize, k, grouped) != LB_OK) return LB_ERR_PROB_SHAPE;
+  if (m == 0 || n == 0 || k == 0) return LB_OK;
+  if (m > 65535LL * 128 || n > (1LL << 30) || k > (1LL << 30)) return LB_ERR_ARG;
+  if (!a || !b || !s) return LB_ERR_ARG;
+  if (var == V_ARGMAX ? (!argmax_state || !argmax_out) : !c) return LB_ERR_ARG;
+  if (!lbh::aligned(a, 16) || !lbh::aligned(b, 16) || !lbh::aligned(s, 16) || (c && !lbh::aligned(c, 2)))
+    return LB_ERR_ALIGN;
+  const Plan pl = make_plan(m, n, k, workspace_len);
+  if (workspace_len < counters_needed(pl, var == V_ARGMAX)) return LB_ERR_WORKSPACE;
+  const size_t need = pl.partial_bytes + (var == V_ARGMAX ? pl.keys_bytes : 0);
+  if (need > 0 && (!scratch || scratch_bytes < need)) return LB_ERR_SCRATCH;
+  if (need > 0 && !lbh::aligned(scratch, 16)) return LB_ERR_ALIGN;
+
+  unsigned char* sc = reinterpret_cast<unsigned char*>(scratch);
+  float* partial = pl.partial_bytes ? reinterpret_cast<float*>(sc) : nullptr;
+  uint64_t* keys = var == V_ARGMAX ? reinterpret_cast<uint64_t*>(sc + pl.partial_bytes) : nullptr;
+
+  if (pl.skinny) {
+    skinny::Params p{};
+    p.a = a; p.b = reinterpret_cast<const uint32_t*>(b); p.s = s; p.c = c;
+    p.counters = workspace; p.partial = partial; p.tile_keys = keys;
+    p.argmax_state = argmax_state; p.argmax_out = argmax_out;
+    p.m = (int)m; p.n = (int)n; p.k = (int)k; p.grouped = grouped; p.splits = pl.splits;
+    p.kp_total = (int)(k / 32); p.n_cg = pl.n_cg;
+    dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
+#define LB_SK(AMV, EPV) hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, EPV>), grid, dim3(skinny::kThreads), pl.lds, st, p)
+    if (var == V_PLAIN) LB_SK(skinny::A_PLAIN, skinny::EPI_STORE);
+    else if (var == V_SILU) LB_SK(skinny::A_SILU_PACKED, skinny::EPI_STORE);
+    else LB_SK(skinny::A_PLAIN, skinny::EPI_ARGMAX);
+#undef LB_SK
+    return lbh::launch_status();
+  }
+
+  gemm::Params p{};
+  p.a = a; p.b = reinterpret_cast<const uint32_t*>(b); p.s = s; p.c = c;
+  p.counters = workspace; p.partial = partial; p.tile_keys = keys;
+  p.argmax_state = argmax_state; p.argmax_out = argmax_out;
+  p.m = (int)m; p.n = (int)n; p.k = (int)k; p.grouped = grouped; p.splits = pl.splits;
+  p.kp_total = (int)(k / 32); p.n_cg = pl.n_cg; p.n_mb = pl.n_mb;
+  dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, (unsigned)pl.n_mb);
+#define LB_GM(MBV, AMV, EPV) hipLaunchKernelGGL((gemm::marlin_gemm_kernel<MBV, AMV, EPV>), grid, dim3(gemm::kThreads), 0, st, p)
+#define LB_GM_MB(AMV, EPV)               \
+  do {                                   \
+    if (pl.mb == 8) LB_GM(8, AMV, EPV);  \
+    else if (pl.mb == 4) LB_GM(4, AMV, EPV); \
+    else LB_GM(2, AMV, EPV);             \
+  } while (0)
+  if (var == V_PLAIN) LB_GM_MB(gemm::A_PLAIN, gemm::EPI_STORE);
+  else if (var == V_SILU) LB_GM_MB(gemm::A_SILU_PACKED, gemm::EPI_STORE);
+  else LB_GM_MB(gemm::A_PLAIN, gemm::EPI_ARGMAX);
+#undef LB_GM_MB
+#undef LB_GM
+  return lbh::launch_status();
+}
+
+}  // namespace marlin
+}  // namespace lb
+
+using namespace lb;
+
+extern "C" const char* lb_status_string(int status) {
+  switch (status) {
+    case LB_OK: return "ok";
+    case LB_ERR_PROB_SHAPE: return "problem shape not supported";
+    case LB_ERR_KERN_SHAPE: return "no kernel for this shape";
+    case LB_ERR_ARG: return "invalid argument";
+    case LB_ERR_ALIGN: return "misaligned pointer";
+    case LB_ERR_WORKSPACE: return "workspace too small";
+    case LB_ERR_SCRATCH: return "scratch too small";
+    case LB_ERR_HIP: return "HIP runtime error";
+    default: return "unknown status";
+  }
+}
+
+extern "C" int lb_abi_version(void) { return 1; }
+
+extern "C" size_t lb_marlin_scratch_bytes(int64_t prob_m, int64_t prob_n, int64_t prob_k, int64_t groupsize) {
+  (void)groupsize;
+  if (prob_m <= 0 || prob_n <= 0 || prob_k <= 0 || prob_n % 256 || prob_k % 128) return 0;
+  // Plan with an unconstrained workspace: the largest scratch any plan uses.
+  const marlin::Plan pl = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX);
+  return pl.partial_bytes + pl.keys_bytes;
+}
+
+extern "C" int lb_marlin_gemm(const uint16_t* A, const int32_t* B, uint16_t* C, const uint16_t* s,
+                              int64_t prob_m, int64_t prob_n, int64_t prob_k,
+                              int32_t* workspace, int64_t workspace_len, int64_t groupsize,
+                              void* scratch, size_t scratch_bytes, lb_stream_t stream) {
+  return marlin::run(marlin::V_PLAIN, A, B, C, s, prob_m, prob_n, prob_k, workspace, workspace_len, groupsize,
+                     nullptr, nullptr, scratch, scratch_bytes, (hipStream_t)stream);
+}
+
+extern "C" int lb_marlin_gemm_silu_packed(const uint16_t* mixed, const int32_t* B, uint16_t* C, const uint16_t* s,
+                                          int64_t prob_m, int64_t prob_n, int64_t prob_k,
+                                          int32_t* workspace, int64_t workspace_len, int64_t groupsize,
+                                          void* scratch, size_t scratch_bytes, lb_stream_t stream) {
+  return marlin::run(marlin::V_SILU, mixed, B, C, s, prob_m, prob_n, prob_k, workspace, workspace_len, groupsize,
+                     nullptr, nullptr, scratch, scratch_bytes, (hipStream_t)stream);
+}
+
+extern "C" int lb_marlin_gemm_argmax(const uint16_t* A, const int32_t* B, const uint16_t* s,
+                                     int64_t prob_m, int64_t prob_n, int64_t prob_k,
+                                     int32_t* workspace, int64_t workspace_len, int64_t groupsize,
+                                     int64_t* argmax_state, int64_t* argmax_out,
+                                     int32_t* argmax_sync, int32_t epoch,
+                                     void* scratch, size_t scratch_bytes, lb_stream_t stream) {
+  (void)argmax_sync;
+  if (epoch <= 0) return LB_ERR_ARG;
+  return marlin::run(marlin::V_ARGMAX, A, B, nullptr, s, prob_m, prob_n, prob_k, workspace, workspace_len,
+                     groupsize, argmax_state, argmax_out, scratch, scratch_bytes, (hipStream_t)stream);
+}
+
+extern "C" int lb_marlin_dequant(const int32_t* B, const uint16_t* s, uint16_t* w_nk,
+                                 int64_t prob_n, int64_t prob_k, int64_t groupsize, lb_stream_t stream) {
+  if (prob_n < 0 || prob_k < 0) return LB_ERR_ARG;
+  if (prob_n % 256 || prob_k % 128) return LB_ERR_PROB_SHAPE;
+  int grouped = 0;
+  if (marlin::normalize_group(groupsize, prob_k, grouped) != LB_OK) return LB_ERR_PROB_SHAPE;
+  if (prob_n == 0 || prob_k == 0) return LB_OK;
+  if (!B || !s || !w_nk) return LB_ERR_ARG;
+  const int64_t total = prob_n * prob_k;
+  const int threads = 256;
+  hipLaunchKernelGGL(marlin::dequant_kernel, dim3((unsigned)((total + threads - 1) / threads)), dim3(threads), 0,
+                     (hipStream_t)stream, reinterpret_cast<const uint32_t*>(B), s, w_nk, prob_n, prob_k, grouped);
+  return lbh::launch_status();
+}
+
+namespace {
+struct MlpPlan {
+  int s1, s2;
+  size_t gu_bytes, act_bytes, down_bytes;
+};
+MlpPlan mlp_plan(int64_t batch, int64_t hidden, int64_t inter) {
+  MlpPlan p{};
+  const int64_t c1 = (2 * inter) / 64, c2 = hidden / 64;
+  const int64_t kp1 = hidden / 32, kp2 = inter / 32;
+  p.s1 = (int)std::max<int64_t>(1, std::min<int64_t>(kp1, (2048 + c1 - 1) / c1));
+  p.s2 = (int)std::max<int64_t>(1, std::min<int64_t>(kp2, (2048 + c2 - 1) / c2));
+  p.gu_bytes = marlin::align_up((size_t)p.s1 * batch * 2 * inter * 4);
+  p.act_bytes = marlin::align_up((size_t)batch * inter * 4);
+  p.down_bytes = marlin::align_up((size_t)p.s2 * batch * hidden * 4);
+  return p;
+}
+}  // namespace
+
+extern "C" size_t lb_marlin_mlp_scratch_bytes(int64_t batch, int64_t hidden, int64_t intermediate) {
+  if (batch <= 0 || hidden <= 0 || intermediate <= 0) return 0;
+  const MlpPlan p = mlp_plan(batch, hidden, intermediate);
+  return p.gu_bytes + p.act_bytes + p.down_bytes;
+}
+
+extern "C" int lb_marlin_mlp_streaming(const int32_t* gate_up_qweight, const uint16_t* gate_up_scales,
+                                       const int32_t* down_qweight, const uint16_t* down_scales,
+                                       const uint16_t* x, uint16_t* out, float* accum, int32_t* sync,
+                                       int64_t batch, int64_t hidden, int64_t intermediate,
+                                       int64_t gate_group_size, int64_t down_group_size,
+                                       void* scratch, size_t scratch_bytes, lb_stream_t stream) {
+  (void)accum;
+  (void)sync;
+  if (batch < 0 || hidden <= 0 || intermediate <= 0) return LB_ERR_ARG;
+  // the streaming kernel reads Marlin tiles of 64 output columns and 32-k steps
+  if (hidden % 128 || intermediate % 128 || (2 * intermediate) % 256 || hidden % 256) return LB_ERR_PROB_SHAPE;
+  int gg = 0, dg = 0;
+  if (marlin::normalize_group(gate_group_size, hidden, gg) != LB_OK) return LB_ERR_PROB_SHAPE;
+  if (marlin::normalize_group(down_group_size, intermediate, dg) != LB_OK) return LB_ERR_PROB_SHAPE;
+  if (batch == 0) return LB_OK;
+  if (!gate_up_qweight || !gate_up_scales || !down_qweight || !down_scales || !x || !out) return LB_ERR_ARG;
+  if (!lbh::aligned(gate_up_qweight, 16) || !lbh::aligned(down_qweight, 16)) return LB_ERR_ALIGN;
+  const MlpPlan pl = mlp_plan(batch, hidden, intermediate);
+  if (!scratch || scratch_bytes < pl.gu_bytes + pl.act_bytes + pl.down_bytes) return LB_ERR_SCRATCH;
+  hipStream_t st = (hipStream_t)stream;
+  unsigned char* sc = reinterpret_cast<unsigned char*>(scratch);
+  float* gu = reinterpret_cast<float*>(sc);
+  float* act = reinterpret_cast<float*>(sc + pl.gu_bytes);
+  float* dp = reinterpret_cast<float*>(sc + pl.gu_bytes + pl.act_bytes);
+  const unsigned zb = (unsigned)((batch + marlin::kF32Batch - 1) / marlin::kF32Batch);
+  hipLaunchKernelGGL((marlin::f32_gemv_kernel<false>), dim3((unsigned)(2 * intermediate / 64), pl.s1, zb), dim3(64), 0, st,
+                     reinterpret_cast<const uint32_t*>(gate_up_qweight), gate_up_scales, (const void*)x, gu, (int)batch,
+                     2 * intermediate, hidden, gg, pl.s1);
+  const int64_t na = batch * intermediate;
+  hipLaunchKernelGGL(marlin::mlp_act_kernel, dim3((unsigned)((na + 255) / 256)), dim3(256), 0, st, gu, act, (int)batch,
+                     intermediate, pl.s1);
+  hipLaunchKernelGGL((marlin::f32_gemv_kernel<true>), dim3((unsigned)(hidden / 64), pl.s2, zb), dim3(64), 0, st,
+                     reinterpret_cast<const uint32_t*>(down_qweight), down_scales, (const void*)act, dp, (int)batch,
+                     hidden, intermediate, dg, pl.s2);
+  const int64_t no = batch * hidden;
+  hipLaunchKernelGGL(marlin::f32_finalize_kernel, dim3((unsigned)((no + 255) / 256)), dim3(256), 0, st, dp, out, no,
+                     pl.s2);
+  return lbh::launch_status();
+}

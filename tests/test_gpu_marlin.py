@@ -1,0 +1,229 @@
+"""Parity of the gfx950 Marlin-layout kernels with the CPU oracle.
+
+Calls go through the C ABI (neurova_amd.capi -> liblangburst_lowbit.so) and,
+for the drop-in surface, through the ``langburst_cuda`` module.  Bar: dequantised
+codes bit-exact; outputs within max-abs 1e-2 / rel 1e-3 of the oracle
+(tests/gpu_util.py).  Reference tests followed:
+langburst/tests/test_lowbit_gemv_cuda.py:76-102 (Marlin vs dequant-matmul).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import lowbit_oracle as O
+from tests.gpu_util import assert_close_f16, print_case, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+
+def _ws(dev, n, mult=16):
+    import torch
+
+    return torch.zeros((max(1, n // 128 * mult),), dtype=torch.int32, device=dev)
+
+
+def _scratch(dev, m, n, k, g):
+    import torch
+    from neurova_amd import capi
+
+    return torch.empty((max(1, capi.marlin_scratch_bytes(m, n, k, g)),), dtype=torch.uint8, device=dev)
+
+
+def _run_gemm(dev, x, qw, sp, g):
+    import torch
+    from neurova_amd import capi
+
+    m, k = x.shape
+    n = qw.shape[1] // 2
+    a, b, s = to_dev(x, dev), to_dev(qw, dev), to_dev(sp, dev)
+    c = torch.full((m, n), float("nan"), dtype=torch.float16, device=dev)
+    ws = _ws(dev, n)
+    st = capi.marlin_gemm(a, b, c, s, ws, g, _scratch(dev, m, n, k, g))
+    assert st == 0, capi.status_string(st)
+    torch.cuda.synchronize()
+    assert int(ws.abs().sum()) == 0, "workspace must be left zero"
+    return to_np(c)
+
+
+@pytest.mark.parametrize("group", [128, -1])
+def test_dequant_bit_exact(dev, group):
+    import torch
+    from neurova_amd import capi
+
+    k, n = 512, 768
+    print_case("dequant", k, n, group)
+    codes, qw, s_nat, sp, _ = O.make_marlin_inputs(1, k, n, group, seed=21)
+    w = torch.empty((n, k), dtype=torch.float16, device=dev)
+    assert capi.marlin_dequant(to_dev(qw, dev), to_dev(sp, dev), w, k, group) == 0
+    ref = O.marlin_dequant_f16(qw, sp, group).T
+    assert np.array_equal(to_np(w).view(np.uint16), np.ascontiguousarray(ref).view(np.uint16))
+
+
+@pytest.mark.parametrize("group", [128, -1])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 16])
+@pytest.mark.parametrize("k,n", [(256, 256), (1024, 512), (512, 1280)])
+def test_skinny_vs_oracle(dev, m, k, n, group):
+    print_case("skinny", m, k, n, group)
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=100 + m + k + n)
+    got = _run_gemm(dev, x, qw, sp, group)
+    exact = assert_close_f16(got, O.marlin_gemm(x, qw, sp, group), what=f"m={m} k={k} n={n} g={group}")
+    assert exact > 0.95
+
+
+@pytest.mark.parametrize("m", [17, 33, 64, 100, 256, 300])
+def test_gemm_vs_oracle(dev, m):
+    k, n = 1024, 768
+    print_case("gemm", m, k, n)
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=300 + m)
+    got = _run_gemm(dev, x, qw, sp, 128)
+    exact = assert_close_f16(got, O.marlin_gemm(x, qw, sp, 128), what=f"m={m}")
+    assert exact > 0.95
+
+
+@pytest.mark.parametrize("m", [1, 4, 16])
+def test_decode_shape_cfg2(dev, m):
+    """M in {1,4,16}, K=5120, N=17408, g=128."""
+    k, n = 5120, 17408
+    print_case("cfg2", m, k, n)
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=7)
+    got = _run_gemm(dev, x, qw, sp, 128)
+    exact = assert_close_f16(got, O.marlin_gemm(x, qw, sp, 128), what=f"cfg2 m={m}")
+    assert exact > 0.95
+
+
+@pytest.mark.parametrize("k,n", [(5120, 17408), (17408, 5120)])
+def test_prefill_shape_cfg3(dev, k, n):
+    """M=2048; a bounded row sample is checked against the oracle."""
+    m = 2048
+    print_case("cfg3", m, k, n)
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=9)
+    got = _run_gemm(dev, x, qw, sp, 128)
+    rows = np.array([0, 1, 15, 16, 127, 128, 1000, 1023, 1024, 2046, 2047])
+    exact = assert_close_f16(got[rows], O.marlin_gemm(x, qw, sp, 128, rows=rows), what=f"cfg3 k={k}")
+    assert exact > 0.95
+
+
+def test_deterministic_split_k(dev):
+    k, n, m = 17408, 5120, 1
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=3)
+    a = _run_gemm(dev, x, qw, sp, 128)
+    b = _run_gemm(dev, x, qw, sp, 128)
+    assert np.array_equal(a.view(np.uint16), b.view(np.uint16))
+
+
+def test_m_zero_is_noop(dev):
+    import torch
+    from neurova_amd import capi
+
+    b = torch.zeros((16, 512), dtype=torch.int32, device=dev)
+    s = torch.zeros((2, 256), dtype=torch.float16, device=dev)
+    a = torch.zeros((0, 256), dtype=torch.float16, device=dev)
+    c = torch.zeros((0, 256), dtype=torch.float16, device=dev)
+    assert capi.marlin_gemm(a, b, c, s, _ws(dev, 256), 128) == 0
+
+
+@pytest.mark.parametrize("m", [1, 5, 40])
+def test_silu_packed_vs_oracle(dev, m):
+    import torch
+    from neurova_amd import capi
+
+    k, n = 1024, 512
+    print_case("silu", m, k, n)
+    _, qw, _, sp, _ = O.make_marlin_inputs(m, k, n, 128, seed=50 + m)
+    mixed = np.random.default_rng(m).normal(0, 1, (m, 2 * k)).astype(np.float16)
+    c = torch.empty((m, n), dtype=torch.float16, device=dev)
+    st = capi.marlin_gemm_silu_packed(to_dev(mixed, dev), to_dev(qw, dev), c, to_dev(sp, dev), _ws(dev, n), 128,
+                                      _scratch(dev, m, n, k, 128))
+    assert st == 0
+    assert_close_f16(to_np(c), O.marlin_gemm_silu_packed(mixed, qw, sp, k, 128), what=f"silu m={m}")
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 1024, 65536), (3, 512, 4096), (16, 256, 2048), (40, 512, 1024)])
+def test_argmax_vs_oracle(dev, m, k, n):
+    import torch
+    from neurova_amd import capi
+
+    print_case("argmax", m, k, n)
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=60 + m)
+    state = torch.zeros((m,), dtype=torch.int64, device=dev)
+    out = torch.full((m,), -1, dtype=torch.int64, device=dev)
+    sync = torch.empty((2,), dtype=torch.int32, device=dev)
+    ws = _ws(dev, n)
+    for epoch in (1, 2):  # two calls in a row reuse the workspace
+        st = capi.marlin_gemm_argmax(to_dev(x, dev), to_dev(qw, dev), to_dev(sp, dev), ws, 128, state, out, sync,
+                                     epoch, _scratch(dev, m, n, k, 128))
+        assert st == 0
+        torch.cuda.synchronize()
+        assert np.array_equal(to_np(out), O.marlin_gemm_argmax(x, qw, sp, 128))
+        assert int(ws.abs().sum()) == 0
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+def test_mlp_streaming_vs_oracle(dev, batch):
+    import torch
+    from neurova_amd import capi
+
+    hidden, inter = 256, 512
+    print_case("mlp", batch, hidden, inter)
+    rng = np.random.default_rng(batch)
+    gu_codes = rng.integers(0, 16, size=(hidden, 2 * inter), dtype=np.uint8)
+    d_codes = rng.integers(0, 16, size=(inter, hidden), dtype=np.uint8)
+    gu_s = (np.abs(rng.normal(0, 0.01, (hidden // 128, 2 * inter))) + 1e-3).astype(np.float16)
+    d_s = (np.abs(rng.normal(0, 0.01, (inter // 128, hidden))) + 1e-3).astype(np.float16)
+    gu_q, d_q = O.marlin_pack_codes(gu_codes), O.marlin_pack_codes(d_codes)
+    gu_sp, d_sp = O.marlin_pack_scales(gu_s), O.marlin_pack_scales(d_s)
+    x = rng.normal(0, 1, (batch, hidden)).astype(np.float16)
+    out = torch.empty((batch, hidden), dtype=torch.float16, device=dev)
+    accum = torch.empty((batch, hidden), dtype=torch.float32, device=dev)
+    sync = torch.zeros((2 * batch,), dtype=torch.int32, device=dev)
+    scratch = torch.empty((capi.marlin_mlp_scratch_bytes(batch, hidden, inter),), dtype=torch.uint8, device=dev)
+    st = capi.marlin_mlp_streaming(to_dev(gu_q, dev), to_dev(gu_sp, dev), to_dev(d_q, dev), to_dev(d_sp, dev),
+                                   to_dev(x, dev), out, accum, sync, hidden, inter, 128, 128, scratch)
+    assert st == 0
+    ref = O.marlin_mlp_streaming(x, gu_q, gu_sp, d_q, d_sp, hidden, inter, 128, 128)
+    assert_close_f16(to_np(out), ref, what="mlp")
+
+
+def test_dropin_module_marlin_ops(dev):
+    """The reference's Python surface: allocating op, _out op, silu_packed_out, argmax_out."""
+    import torch
+    import langburst_cuda as lc
+
+    m, k, n = 4, 1024, 512
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=77)
+    q, s, xd = to_dev(qw, dev), to_dev(sp, dev), to_dev(x, dev)
+    ref = O.marlin_gemm(x, qw, sp, 128)
+    y = lc.lowbit_marlin_gemm(q, s, xd, k, 128)
+    assert_close_f16(to_np(y), ref, what="lowbit_marlin_gemm")
+    out = torch.empty((m, n), dtype=torch.float16, device=dev)
+    ws = torch.zeros((n // 128 * 16,), dtype=torch.int32, device=dev)
+    lc.lowbit_marlin_gemm_out(qweight=q, scales=s, x=xd, out=out, workspace=ws, cols=k, group_size=128)
+    assert np.array_equal(to_np(out).view(np.uint16), to_np(y).view(np.uint16))
+    mixed = np.random.default_rng(1).normal(0, 1, (m, 2 * k)).astype(np.float16)
+    lc.lowbit_marlin_gemm_silu_packed_out(q, s, to_dev(mixed, dev), out, ws, k, 128)
+    assert_close_f16(to_np(out), O.marlin_gemm_silu_packed(mixed, qw, sp, k, 128), what="silu_packed_out")
+    state = torch.empty((m,), dtype=torch.int64, device=dev)
+    am = torch.empty((m,), dtype=torch.int64, device=dev)
+    sync = torch.empty((2,), dtype=torch.int32, device=dev)
+    lc.lowbit_marlin_gemm_argmax_out(q, s, xd, out, ws, state, am, sync, 1, k, 128)
+    assert np.array_equal(to_np(am), ref.astype(np.float32).argmax(axis=1))
+    with pytest.raises(RuntimeError, match="Marlin requires K divisible by 128"):
+        lc.lowbit_marlin_gemm(q, s, xd[:, :100].contiguous(), 100, 128)
+    with pytest.raises(RuntimeError, match="Marlin supports group_size -1 or 128"):
+        lc.lowbit_marlin_gemm(q, s, xd, k, 64)
+    w = lc.lowbit_marlin_dequant(q, s, k, 128)
+    assert np.array_equal(to_np(w).view(np.uint16), np.ascontiguousarray(O.marlin_dequant_f16(qw, sp, 128).T).view(np.uint16))
+
+
+def test_single_hip_runtime_in_process(dev):
+    """The C-ABI library must bind to the HIP runtime PyTorch loaded, not a second copy."""
+    import neurova_amd  # noqa: F401
+    from neurova_amd import capi
+
+    capi.lib()
+    maps = open("/proc/self/maps").read().splitlines()
+    hip = {line.split()[-1] for line in maps if "libamdhip64" in line}
+    assert len(hip) == 1, hip
+    ours = {line.split()[-1] for line in maps if "liblangburst_lowbit" in line or "langburst_cuda" in line}
+    assert len(ours) == 2, ours
