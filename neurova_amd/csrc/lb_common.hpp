@@ -28,6 +28,38 @@ __device__ __forceinline__ uint16_t f2h(float f) { return __builtin_bit_cast(uin
 // the fp16 pair (code - 8): OR-ing the exponent of 1024 turns the nibble into the
 // mantissa of 1024 + code; subtracting 1032 is exact.  Codes in bits [4,8) and
 // [20,24) give 1024 + 16*code, scaled by 1/16 and offset by -72 with one exact fma.
+// The mask-and-OR is a single v_and_or_b32 (mask in an SGPR, the exponent
+// pattern in a VGPR: gfx9 VOP3 takes no literals and one scalar operand).
+__device__ __forceinline__ uint32_t and_or(uint32_t w, uint32_t smask, uint32_t vbits) {
+  uint32_t r;
+  asm("v_and_or_b32 %0, %1, %2, %3" : "=v"(r) : "v"(w), "s"(smask), "v"(vbits));
+  return r;
+}
+struct NibConsts {
+  uint32_t lo_mask, hi_mask;  // SGPR
+  uint32_t magic;             // VGPR 0x64006400
+};
+__device__ __forceinline__ NibConsts nib_consts() {
+  NibConsts c;
+  asm("s_mov_b32 %0, 0x000f000f" : "=s"(c.lo_mask));
+  asm("s_mov_b32 %0, 0x00f000f0" : "=s"(c.hi_mask));
+  asm("v_mov_b32 %0, 0x64006400" : "=v"(c.magic));
+  return c;
+}
+__device__ __forceinline__ f16x2 nib_lo_to_h2(uint32_t w, const NibConsts& k) {
+  return as_h2(and_or(w, k.lo_mask, k.magic)) - (f16x2){(f16)1032.0f, (f16)1032.0f};
+}
+__device__ __forceinline__ f16x2 nib_hi_to_h2(uint32_t w, const NibConsts& k) {
+  return as_h2(and_or(w, k.hi_mask, k.magic)) * (f16x2){(f16)0.0625f, (f16)0.0625f} + (f16x2){(f16)-72.0f, (f16)-72.0f};
+}
+// Biased forms: 1024 + code (bits [0,4) / [16,20)) and 1024 + 16*code
+// (bits [4,8) / [20,24)), one v_and_or_b32 each; the caller removes the bias.
+__device__ __forceinline__ f16x2 nib_lo_biased(uint32_t w, const NibConsts& k) {
+  return as_h2(and_or(w, k.lo_mask, k.magic));
+}
+__device__ __forceinline__ f16x2 nib_hi_biased(uint32_t w, const NibConsts& k) {
+  return as_h2(and_or(w, k.hi_mask, k.magic));
+}
 __device__ __forceinline__ f16x2 nib_lo_to_h2(uint32_t w) {
   const uint32_t v = (w & 0x000f000fu) | 0x64006400u;
   return as_h2(v) - (f16x2){(f16)1032.0f, (f16)1032.0f};
@@ -54,16 +86,48 @@ __device__ __forceinline__ float wave_sum(float v) {
   return v + __builtin_bit_cast(float, __builtin_amdgcn_ds_bpermute((lane ^ 32) << 2, __builtin_bit_cast(int, v)));
 }
 
-// Device-scope (all XCDs) release of this workgroup's global writes followed by
-// an arrival count on `counter`; returns the count before this arrival.
-// Call from one thread after a __syncthreads() that follows the writes.
-__device__ __forceinline__ int arrive_release(int* counter) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "agent");
+// Cross-workgroup hand-off without cache-wide fences.
+//
+// A device-scope release/acquire fence costs an L2 write-back / invalidate on
+// every XCD (buffer_wbl2 / buffer_inv).  Those exist for ordinary accesses;
+// here every word that crosses workgroups is itself a device-scope atomic
+// access: relaxed agent-scope atomic stores and loads, which gfx950 performs
+// as stores/loads with the device-coherence bit (sc1) at full store/load
+// bandwidth.  A workgroup publishes its partials with such stores, waits until
+// they are acknowledged (vmcnt counts stores on gfx9), and only then counts
+// its arrival with an atomic add (a read-modify-write, always performed at
+// device scope); the workgroup that observes the final count reads the
+// partials with device-scope atomic loads and resets the counter with an
+// atomic swap whose return it also waits for, so the next launch starts from
+// zero.
+__device__ __forceinline__ void publish(float* p, float v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void publish(uint64_t* p, uint64_t v) {
+  __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ float collect(const float* p) {
+  return __hip_atomic_load(const_cast<float*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ uint64_t collect(const uint64_t* p) {
+  return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Waits until every vector-memory operation this thread issued (loads,
+// stores, atomics) has been acknowledged; the memory clobber keeps the
+// compiler from moving memory accesses across it.
+__device__ __forceinline__ void wait_published() { asm volatile("s_waitcnt vmcnt(0)" : : : "memory"); }
+
+// Counts this workgroup's arrival on `counter`; returns the count before it.
+__device__ __forceinline__ int arrive(int* counter) {
   return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
-// Device-scope acquire: later loads observe writes released by other workgroups.
-__device__ __forceinline__ void acquire_device() { __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "agent"); }
+// Zeroes a counter and waits for the swap to be performed.
+__device__ __forceinline__ void reset_counter(int* counter) {
+  const int old = __hip_atomic_exchange(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  asm volatile("s_waitcnt vmcnt(0)" : : "v"(old) : "memory");
+}
 
 }  // namespace lb
 

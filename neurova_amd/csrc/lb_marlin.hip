@@ -4,6 +4,8 @@
 
 #include <stdlib.h>
 
+#include <algorithm>
+
 #include "marlin_gemm.hpp"
 #include "marlin_skinny.hpp"
 
@@ -156,30 +158,59 @@ struct Plan {
   int n_cg = 0;
   int splits = 1;
   size_t lds = 0;    // decode kernel dynamic LDS
+  size_t x_bytes = 0; // decode kernel: staged activations
   size_t partial_bytes = 0;
   size_t keys_bytes = 0;
 };
 
-constexpr int kSkinnyTargetWGs = 512;  // 2048 waves: ~8 per CU
-constexpr int kGemmTargetWGs = 512;    // two workgroups per CU
+#ifndef LB_SKINNY_WGS_PER_CU
+#define LB_SKINNY_WGS_PER_CU 2    // decode workgroups resident per CU (register-limited)
+#endif
+#ifndef LB_GEMM_TARGET_WGS
+#define LB_GEMM_TARGET_WGS 512    // two workgroups per CU
+#endif
+constexpr int kSkinnyWGsPerCU = LB_SKINNY_WGS_PER_CU;
+constexpr int kGemmTargetWGs = LB_GEMM_TARGET_WGS;
 constexpr size_t kSkinnyMaxX = 48 * 1024;
+
+// Compute units of the current device (cached per device; 256 on a full MI355X,
+// fewer in a compute-partitioned mode).
+inline int device_cus() {
+  static int cache[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  int v = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
+  if (v <= 0) {
+    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
+    __atomic_store_n(&cache[dev], v, __ATOMIC_RELAXED);
+  }
+  return v;
+}
 
 inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
   Plan pl;
   pl.n_cg = (int)(n / 256);
   const int groups = (int)(k / 128);
-  if (m <= skinny::kMaxM) {
+  const bool can_split = workspace_len >= (int64_t)pl.n_cg + 1;
+  const size_t x_all = (size_t)k * (size_t)m * 2;
+  // The decode kernel stages its whole A slice in LDS: without the workspace
+  // to split K, a slice too large for LDS goes to the GEMM kernel instead.
+  if (m <= skinny::kMaxM && (can_split || x_all <= kSkinnyMaxX)) {
     pl.skinny = true;
-    int s = (kSkinnyTargetWGs + pl.n_cg - 1) / pl.n_cg;
-    const size_t x_all = (size_t)k * (size_t)m * 2;
+    // As many k splits as fit in one wave of resident workgroups: a second,
+    // partial wave would cost a whole workgroup's time for a few tiles.
+    int s = (kSkinnyWGsPerCU * device_cus()) / pl.n_cg;
     const int s_lds = (int)((x_all + kSkinnyMaxX - 1) / kSkinnyMaxX);
     if (s < s_lds) s = s_lds;
     if (s > groups) s = groups;
     if (s < 1) s = 1;
-    if (s > 1 && workspace_len < (int64_t)pl.n_cg + 1) s = 1;
+    if (!can_split) s = 1;
     pl.splits = s;
     const int max_groups = (groups + s - 1) / s;
-    pl.lds = (size_t)max_groups * 128 * (size_t)m * 2 + skinny::kWaves * 64 * 16;
+    pl.x_bytes = (size_t)max_groups * 128 * (size_t)m * 2;  // staged A slice
+    // + the zero entry + the bias corrections [group][16] fp32
+    const size_t stage = pl.x_bytes + 16 + (size_t)max_groups * skinny::kMaxM * 4;
+    pl.lds = std::max(stage, (size_t)m * skinny::kCols * 4);
   } else {
     pl.skinny = false;
     pl.mb = m > 64 ? 8 : (m > 32 ? 4 : 2);
@@ -247,13 +278,15 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
     p.a = a; p.b = reinterpret_cast<const uint32_t*>(b); p.s = s; p.c = c;
     p.counters = workspace; p.partial = partial; p.tile_keys = keys;
     p.argmax_state = argmax_state; p.argmax_out = argmax_out;
-    p.m = (int)m; p.n = (int)n; p.k = (int)k; p.grouped = grouped; p.splits = pl.splits;
+    p.m = (int)m; p.n = (int)n; p.k = (int)k; p.splits = pl.splits;
     p.kp_total = (int)(k / 32); p.n_cg = pl.n_cg;
     dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
-#define LB_SK(AMV, EPV) hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, EPV>), grid, dim3(skinny::kThreads), pl.lds, st, p)
-    if (var == V_PLAIN) LB_SK(skinny::A_PLAIN, skinny::EPI_STORE);
-    else if (var == V_SILU) LB_SK(skinny::A_SILU_PACKED, skinny::EPI_STORE);
-    else LB_SK(skinny::A_PLAIN, skinny::EPI_ARGMAX);
+#define LB_SK(AMV, EPV, GV) hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, EPV, GV>), grid, dim3(skinny::kThreads), pl.lds, st, p)
+#define LB_SKG(AMV, EPV) do { if (grouped) LB_SK(AMV, EPV, true); else LB_SK(AMV, EPV, false); } while (0)
+    if (var == V_PLAIN) LB_SKG(skinny::A_PLAIN, skinny::EPI_STORE);
+    else if (var == V_SILU) LB_SKG(skinny::A_SILU_PACKED, skinny::EPI_STORE);
+    else LB_SKG(skinny::A_PLAIN, skinny::EPI_ARGMAX);
+#undef LB_SKG
 #undef LB_SK
     return lbh::launch_status();
   }

@@ -143,6 +143,7 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
   // B fragment source: slots 4cc + 2gq and +1 of row 2kp + prow of this chunk
   const uint32_t* bsrc = p.b + (int64_t)prow * row_words + (int64_t)chunk * 128 + (cc * 4 + gq * 2) * 4;
   const uint16_t* ssrc = p.s + chunk * 64 + cc * 8;
+  const NibConsts nk = nib_consts();
 
   // A staging assignment: (row, half) pairs, BM*2 of them over 256 threads
   constexpr int kAItems = BM * 2;
@@ -215,10 +216,10 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
     for (int j = 0; j < 4; ++j) {
       const uint32_t v0 = bcur0[j] >> sh;
       const uint32_t v1 = bcur1[j] >> sh;
-      f16x2 b0 = nib_lo_to_h2(v0);
-      f16x2 b1 = nib_lo_to_h2(v1);
-      f16x2 b2 = nib_hi_to_h2(v0);
-      f16x2 b3 = nib_hi_to_h2(v1);
+      f16x2 b0 = nib_lo_to_h2(v0, nk);
+      f16x2 b1 = nib_lo_to_h2(v1, nk);
+      f16x2 b2 = nib_hi_to_h2(v0, nk);
+      f16x2 b3 = nib_hi_to_h2(v1, nk);
       if (p.grouped) {
         b0 *= sc[j];
         b1 *= sc[j];
@@ -252,14 +253,14 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int r = rbase + 16 * i + e;
-          if (r < p.m) part[(int64_t)r * p.n + ccol + 16 * j] = acc[j][i][e];
+          if (r < p.m) publish(part + (int64_t)r * p.n + ccol + 16 * j, acc[j][i][e]);
         }
+    wait_published();
     __syncthreads();
     int32_t* ctr = p.counters + 1 + cg + mb * p.n_cg;
-    if (tid == 0) s_prev = arrive_release(ctr);
+    if (tid == 0) s_prev = arrive(ctr);
     __syncthreads();
     if (s_prev != p.splits - 1) return;
-    acquire_device();
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
@@ -270,11 +271,11 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
           float sum = 0.f;
           if (r < p.m) {
             for (int sp = 0; sp < p.splits; ++sp)
-              sum += __builtin_nontemporal_load(p.partial + ((int64_t)sp * p.m + r) * p.n + ccol + 16 * j);
+              sum += collect(p.partial + ((int64_t)sp * p.m + r) * p.n + ccol + 16 * j);
           }
           acc[j][i][e] = sum;
         }
-    if (tid == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    if (tid == 0) reset_counter(ctr);
   }
 
   float colscale[4] = {1.f, 1.f, 1.f, 1.f};
@@ -326,19 +327,19 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
       uint64_t best = 0;
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) best = max_u64(best, s_keys[w][rl]);
-      p.tile_keys[(int64_t)r * p.n_cg + cg] = best;
+      publish(p.tile_keys + (int64_t)r * p.n_cg + cg, best);
     }
   }
+  wait_published();
   __syncthreads();
   int32_t* final_counter = p.counters;
-  if (tid == 0) s_prev = arrive_release(final_counter);
+  if (tid == 0) s_prev = arrive(final_counter);
   __syncthreads();
   if (s_prev != p.n_cg * p.n_mb - 1) return;
-  acquire_device();
   for (int r = wave; r < p.m; r += kWaves) {
     uint64_t best = 0;
     for (int t = lane; t < p.n_cg; t += kWave)
-      best = max_u64(best, __builtin_nontemporal_load(p.tile_keys + (int64_t)r * p.n_cg + t));
+      best = max_u64(best, collect(p.tile_keys + (int64_t)r * p.n_cg + t));
 #pragma unroll
     for (int off = 1; off < 64; off <<= 1) best = max_u64(best, shfl_xor_u64(best, lane, off));
     if (lane == 0) {
@@ -346,7 +347,7 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
       p.argmax_out[r] = (int64_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
     }
   }
-  if (tid == 0) __hip_atomic_store(final_counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  if (tid == 0) reset_counter(final_counter);
 }
 
 }  // namespace gemm

@@ -1,5 +1,4 @@
-// Marlin-layout W4A16 projection for skinny batches (decode: M <= 16 per
-// 16-row block) on gfx950.
+// Marlin-layout W4A16 projection for skinny batches (decode: M <= 16) on gfx950.
 //
 // Reads the reference's Marlin layout (langburst/csrc/marlin_cuda_kernel.cu,
 // packing in adapters/qwen36_tools/quantize.py:180-243) directly; no repack.
@@ -8,29 +7,43 @@
 //   qweight int32 [K/16, 2N].  Row kb holds k = 16kb..16kb+15.  Each 64-column
 //   "chunk" of a row is 128 int32 = 512 contiguous bytes = 32 16-byte slots.
 //   Slot i (0..31), with c = i>>2 and q = i&3, holds 4 words j = 0..3; word j
-//   covers columns 16j+c (nibbles 0,1,4,5) and 16j+c+8 (nibbles 2,3,6,7) of
-//   the chunk at k-offsets {2q, 2q+8, 2q+1, 2q+9} (low nibble of bytes 0/2 =
-//   k 2q/2q+1, high nibble = k 2q+8/2q+9; bytes 1/3 the same for column +8).
-//   Group scales: 64-column chunk of row g stores column 8jj+i at 8i+jj, so
-//   the 8 scales a slot needs are the 16 bytes at 8c.
+//   covers columns 16j+c (bytes 0,2) and 16j+c+8 (bytes 1,3) of the chunk:
+//   the low nibbles of bytes 0/2 are k = 2q / 2q+1, the high nibbles
+//   k = 2q+8 / 2q+9.  Group scales: the 64-column chunk of group row g stores
+//   column 8jj+i at 8i+jj, so the 8 scales a slot needs are the 16 bytes at 8c.
 //
-// Kernel structure.  A workgroup owns 4 chunks (256 columns) and a range of
-// k; wave w streams chunk w.  Per 32-k step a wave loads 1 KB of qweight with
-// fully coalesced 16-byte loads (rows kb and kb+1), bounces it through a
-// wave-private 1 KB LDS slot, and each lane reads the two adjacent slots its
-// MFMA B fragment needs.  The fragment of v_mfma_f32_16x16x32_f16 (lane
-// l = 16g + nl holds 8 k-values of column nl) is built in registers:
-// k-group g = (row p = g>>1, slot pair q = 2(g&1), 2(g&1)+1), column
-// nl = 8h + c, so its 8 halves are (q0 k0,k1)(q1 k0,k1)(q0 k8,k9)(q1 k8,k9)
-// = physical k 4g'+{0,1,2,3} and 4g'+8+{0,1,2,3} of row p -- two contiguous
-// 8-byte runs of the activation row, which is staged in LDS as
-// [k/4][m][4 halves].  Dequant is the exact fp16 (q-8), then one fp16 multiply
-// by the group scale: the same rounding as the reference's __hmul2.
+// Kernel.  A workgroup owns 4 chunks (256 columns) and a k range; wave w
+// streams chunk w.  The B fragment of v_mfma_f32_16x16x32_f16 (lane
+// l = 16g + nl holds 8 k-values of column nl) is built in registers: with
+// k-group g = (row p = g>>1, slot pair 4c+2g', 4c+2g'+1, g' = g&1) and column
+// nl = 8h + c, the fragment needs the h half of every word of both slots of
+// the pair: (q0 k0,k1)(q1 k0,k1)(q0 k8,k9)(q1 k8,k9) = physical k 4g'+{0..3}
+// and 4g'+8+{0..3} of row p.  Lane l loads only slot 4c+2g'+h, so the 32
+// lanes of a row fetch its 512 bytes once; the other slot of the pair is in
+// lane l^8 and arrives by a DPP row rotation, and one v_perm_b32 gathers the
+// four bytes the lane uses.  Dequant is one v_and_or_b32 per fp16 pair, which
+// yields the exact biased values 1024 + q (k = 0..7 of a row, low nibbles) and
+// 1024 + 16q (k = 8..15, high nibbles); the A slice is staged with its
+// k = 8..15 halves scaled by 1/16, and each scale group's MFMAs start from
+// -(1032 * sum of the low-half activations + 1152 * sum of the staged high-half
+// ones), which removes the bias and leaves the sum of x * (q - 8) accumulated
+// in fp32.  The group's scale then multiplies that fp32 sum once
+// (the reference rounds each fp16 (q-8)*s before the MMA; the two differ by
+// that rounding, far inside fp16 output precision).
 //
-// Split-K.  When the k range is split over S workgroups, each writes fp32
-// partials to scratch [S][M][N]; the last workgroup to arrive on the
-// column-group counter (workspace, zero on entry) sums them in split order
-// (deterministic), writes the fp16 result and re-zeroes the counter.
+// Latency.  The activation slice of the workgroup's k range is staged once in
+// LDS in fragment order ([k/32][4 k-groups][m] x 16 bytes, SiLU-gated
+// variant: fp16(silu(g) * u)); the staging loads are issued first and the
+// first weight batches (one scale group, 1 KB per wave each) right behind
+// them, so the staging round trip overlaps the weight fetch.  A ring of
+// kDepth batches stays in flight, with unconditional loads, so the memory
+// counters never force a full drain.
+
+// Epilogue.  Accumulators go through LDS so that thread t owns output column
+// t of the workgroup's 256.  Under split-K each workgroup publishes fp32
+// partials to scratch [S][M][N]; the last one to arrive on the tile's counter
+// (workspace, zero on entry and on exit) collects them in split order
+// (deterministic), rounds to fp16 and stores or feeds the fused argmax.
 
 #pragma once
 #include "lb_common.hpp"
@@ -40,9 +53,18 @@ namespace skinny {
 
 constexpr int kWaves = 4;               // chunks (64 columns each) per workgroup
 constexpr int kThreads = kWaves * kWave;
-constexpr int kColsPerWG = 64 * kWaves;  // 256
-constexpr int kMaxM = 16;                // rows per m-block (MFMA tile height)
-constexpr int kPrefetch = 4;             // 1 KB steps in flight per batch (x2 double buffer)
+constexpr int kCols = 64 * kWaves;      // 256 columns per workgroup
+constexpr int kMaxM = 16;               // rows of the MFMA tile
+constexpr int kSteps = 4;               // 32-k steps per batch (one scale group)
+constexpr int kStageUnroll = 8;         // A staging: 16-byte items in flight per thread
+#ifndef LB_SKINNY_DEPTH
+#define LB_SKINNY_DEPTH 2
+#endif
+constexpr int kDepth = LB_SKINNY_DEPTH;  // weight batches in flight
+
+#ifndef LB_STREAM_LOADS
+#define LB_STREAM_LOADS 0               // non-temporal weight loads (measured slower)
+#endif
 
 enum AMode { A_PLAIN = 0, A_SILU_PACKED = 1 };
 enum EpiMode { EPI_STORE = 0, EPI_ARGMAX = 1 };
@@ -58,7 +80,6 @@ struct Params {
   int64_t* argmax_state; // [M]
   int64_t* argmax_out;   // [M]
   int m, n, k;
-  int grouped;           // 1: group size 128, 0: one scale per column
   int splits;            // S
   int kp_total;          // K / 32
   int n_cg;              // N / 256
@@ -95,273 +116,330 @@ __device__ __forceinline__ void split_range(const Params& p, int split, int& kp0
   kp1 = g1 << 2;
 }
 
-template <int AM, int EPI>
+// Inverse of the per-column scale permutation (quantize.py:66-68).
+__device__ __forceinline__ int per_column_scale_index(int n) {
+  const int r = n & 31;
+  return (n & ~31) + 8 * ((r >> 1) & 3) + ((r >> 3) << 1) + (r & 1);
+}
+
+__device__ __forceinline__ uint32_t silu_mul2(uint32_t g, uint32_t u) {
+  const float g0 = h2f((uint16_t)(g & 0xffffu)), g1 = h2f((uint16_t)(g >> 16));
+  const float u0 = h2f((uint16_t)(u & 0xffffu)), u1 = h2f((uint16_t)(u >> 16));
+  return (uint32_t)f2h(silu(g0) * u0) | ((uint32_t)f2h(silu(g1) * u1) << 16);
+}
+
+template <int AM, int EPI, bool GROUPED>
 __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  __shared__ int s_prev;
+  __shared__ uint64_t s_keys[kWaves][kMaxM];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int cg = blockIdx.x;      // column group (256 columns)
+  const int cg = blockIdx.x;  // column group (256 columns)
   const int split = blockIdx.y;
-  const int mb = blockIdx.z;      // 16-row block of A
-  const int m0 = mb * kMaxM;
-  const int mrows = min(kMaxM, p.m - m0);
+  const int mrows = p.m;      // <= kMaxM
 
   int kp0, kp1;
   split_range(p, split, kp0, kp1);
-  const int nkp = kp1 - kp0;
-  const int k0 = kp0 * 32;
-  const int kr = nkp * 32;
-
-  // ---- stage A rows [m0, m0+mrows) x [k0, k0+kr) as xs[k/4][m][4 halves] ----
-  uint2* xs = reinterpret_cast<uint2*>(smem);
-  uint4* bstage = reinterpret_cast<uint4*>(smem + (size_t)kr * mrows * 2);  // kWaves x 64 x 16 B
-  {
-    const int quads = kr >> 2;
-    const int items = quads * mrows;
-    for (int it = tid; it < items; it += kThreads) {
-      const int mm = it / quads;
-      const int kq = it - mm * quads;
-      const int kk = k0 + (kq << 2);
-      uint2 v;
-      if (AM == A_PLAIN) {
-        v = *reinterpret_cast<const uint2*>(p.a + (int64_t)(m0 + mm) * p.k + kk);
-      } else {
-        const uint16_t* row = p.a + (int64_t)(m0 + mm) * (2 * (int64_t)p.k);
-        const uint2 g = *reinterpret_cast<const uint2*>(row + kk);
-        const uint2 u = *reinterpret_cast<const uint2*>(row + p.k + kk);
-        const uint32_t gw[2] = {g.x, g.y};
-        const uint32_t uw[2] = {u.x, u.y};
-        uint32_t ow[2];
-#pragma unroll
-        for (int w = 0; w < 2; ++w) {
-          const float g0 = h2f((uint16_t)(gw[w] & 0xffffu)), g1 = h2f((uint16_t)(gw[w] >> 16));
-          const float u0 = h2f((uint16_t)(uw[w] & 0xffffu)), u1 = h2f((uint16_t)(uw[w] >> 16));
-          ow[w] = (uint32_t)f2h(silu(g0) * u0) | ((uint32_t)f2h(silu(g1) * u1) << 16);
-        }
-        v = make_uint2(ow[0], ow[1]);
-      }
-      xs[kq * mrows + mm] = v;
-    }
-  }
-  __syncthreads();
-
-  // ---- per-wave stream over one 64-column chunk ----
-  const int chunk = cg * kWaves + wave;
-  const int64_t row_words = 2 * (int64_t)p.n;  // int32 per qweight row
-  // coalesced load: lane L takes slot (L & 31) of row 2*kp + (L >> 5)
-  const uint32_t* bsrc = p.b + (int64_t)(lane >> 5) * row_words + (int64_t)chunk * 128 + (lane & 31) * 4;
-  uint4* my_stage = bstage + wave * 64;
+  const int nkp = kp1 - kp0;  // positive multiple of kSteps
 
   // fragment coordinates: lane = 16g + 8h + c
+  const int chunk = cg * kWaves + wave;
+  const int64_t row_words = 2 * (int64_t)p.n;  // int32 per qweight row
   const int g = lane >> 4;
   const int hsel = (lane >> 3) & 1;
   const int cc = lane & 7;
-  const int prow = g >> 1;     // which of the two k16 rows
-  const int gq = g & 1;        // slot pair (q0, q1) = (2gq, 2gq+1)
-  const int slot0 = prow * 32 + cc * 4 + gq * 2;
+  const int prow = g >> 1;  // which of the two k16 rows of a 32-k step
+  const int gq = g & 1;     // slot pair (q0, q1) = (2gq, 2gq+1)
+  // Each lane loads one slot, 4c + 2gq + h; the pair's other slot comes from
+  // lane ^ 8 (same c and g, other h) by a DPP row rotation.
+  const uint32_t* bsrc = p.b + (int64_t)prow * row_words + (int64_t)chunk * 128 + (cc * 4 + gq * 2 + hsel) * 4;
+  const uint16_t* ssrc = p.s + chunk * 64 + cc * 8;
+  // Byte selection of v_perm_b32(own, partner): word = [A.b_h, B.b_h, A.b_(2+h), B.b_(2+h)]
+  // with A = slot 4c+2gq (q0) and B = slot 4c+2gq+1 (q1).
+  const uint32_t psel = hsel ? 0x07030501u : 0x02060004u;
   const int mrow = lane & 15;  // A fragment row
+  const NibConsts nk = nib_consts();
+
+  // LDS: staged A in fragment order, entry (kp, g, m) = 16 bytes holding
+  // x[m][32kp + 16(g>>1) + 4(g&1) + {0..3}] and, scaled by 1/16, the same +8;
+  // then one zero entry (read by the lanes of rows >= M), then the bias
+  // correction of each scale group of the slice, [group][16 rows] fp32.
+  u32x4* afr = reinterpret_cast<u32x4*>(smem);
+  const int k0 = kp0 * 32;
+  const int octs = nkp * 4;            // 8-half runs per row of the slice
+  const int items = octs * mrows;
+  const int n_frag = nkp * 4 * mrows;  // staged entries; afr[n_frag] is the zero entry
+  float* corr = reinterpret_cast<float*>(afr + n_frag + 1);
+  const int64_t a_row_stride = AM == A_SILU_PACKED ? 2 * (int64_t)p.k : (int64_t)p.k;
+  uint4 gv[kStageUnroll], uv[kStageUnroll];
+  auto stage_load = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const int it = min(base + u * kThreads + tid, items - 1);
+      const int mm = it / octs;
+      const uint16_t* src = p.a + (int64_t)mm * a_row_stride + k0 + ((it - mm * octs) << 3);
+      gv[u] = *reinterpret_cast<const uint4*>(src);
+      if (AM == A_SILU_PACKED) uv[u] = *reinterpret_cast<const uint4*>(src + p.k);
+    }
+  };
+  auto stage_store = [&](int base) {
+#pragma unroll
+    for (int u = 0; u < kStageUnroll; ++u) {
+      const int it = base + u * kThreads + tid;
+      if (it < items) {
+        const int mm = it / octs;
+        const int r = it - mm * octs;  // kp = r >> 2, octet o = r & 3 = 2 prow + half
+        uint4 w = gv[u];
+        if (AM == A_SILU_PACKED)
+          w = make_uint4(silu_mul2(w.x, uv[u].x), silu_mul2(w.y, uv[u].y), silu_mul2(w.z, uv[u].z),
+                         silu_mul2(w.w, uv[u].w));
+        if (GROUPED && (r & 1)) {  // k = 8..15 of the row: these meet the 16x-biased high nibbles
+          const f16x2 q = (f16x2){(f16)0.0625f, (f16)0.0625f};
+          w = make_uint4(as_u32(as_h2(w.x) * q), as_u32(as_h2(w.y) * q), as_u32(as_h2(w.z) * q),
+                         as_u32(as_h2(w.w) * q));
+        }
+        const int fg = ((r >> 2) * 4 + ((r & 3) >> 1) * 2) * mrows + mm;  // fragment (kp, g = 2 prow)
+        uint2* dst = reinterpret_cast<uint2*>(afr + fg) + (r & 1);
+        dst[0] = make_uint2(w.x, w.y);          // halves 0..3 -> g = 2 prow
+        dst[2 * mrows] = make_uint2(w.z, w.w);  // halves 4..7 -> g = 2 prow + 1
+      }
+    }
+  };
+
+  // Ring of kDepth batches (one scale group, 1 KB per wave, each) in flight.
+  u32x4 bw[kDepth][kSteps];
+  u32x4 bs[kDepth];
+#pragma unroll
+  for (int i = 0; i < kDepth; ++i) bs[i] = (u32x4){0, 0, 0, 0};
+  auto issue = [&](u32x4(&w)[kSteps], u32x4& scl, int batch) {
+    const int kpf = kp0 + batch * kSteps;
+#pragma unroll
+    for (int d = 0; d < kSteps; ++d) {
+      const u32x4* src = reinterpret_cast<const u32x4*>(bsrc + (int64_t)(kpf + d) * 2 * row_words);
+#if LB_STREAM_LOADS
+      w[d] = __builtin_nontemporal_load(src);
+#else
+      w[d] = *src;
+#endif
+    }
+    if (GROUPED) scl = *reinterpret_cast<const u32x4*>(ssrc + (int64_t)(kpf >> 2) * p.n);
+  };
+
+  // ---- staging loads, then the first weight batches, then the stores ----
+  const int nb = nkp / kSteps;
+  stage_load(0);
+  __builtin_amdgcn_sched_barrier(0);  // staging loads strictly before the weight loads
+#pragma unroll
+  for (int i = 0; i < kDepth; ++i) issue(bw[i], bs[i], min(i, nb - 1));
+  __builtin_amdgcn_sched_barrier(0);
+  stage_store(0);
+  for (int base = kThreads * kStageUnroll; base < items; base += kThreads * kStageUnroll) {
+    stage_load(base);
+    stage_store(base);
+  }
+  if (tid == 0) afr[n_frag] = (u32x4){0, 0, 0, 0};
+  __syncthreads();
+
+  // Bias correction.  The MFMA sees 1024 + q against x (k = 0..7 of a row) and
+  // 1024 + 16q against x/16 (k = 8..15), i.e. x*q + 1024x and x~*q + 64x~ with
+  // x~ = 16 * fp16(x/16); subtracting 1032*sum(x) + 72*sum(x~) = 1032*lo + 1152*hi
+  // (sums of the staged values) leaves sum(x * (q - 8)).  Fixed-order sums.
+  for (int t = tid; GROUPED && t < nb * kMaxM; t += kThreads) {
+    const int gi = t / kMaxM, mm = t - gi * kMaxM;
+    float lo = 0.f, hi = 0.f;
+    if (mm < mrows) {
+      for (int e = 0; e < 4 * kSteps; ++e) {  // the group's 4 k-steps x 4 fragments
+        const u32x4 f = afr[(gi * 4 * kSteps + e) * mrows + mm];
+        lo += (float)as_h2(f[0])[0] + (float)as_h2(f[0])[1] + (float)as_h2(f[1])[0] + (float)as_h2(f[1])[1];
+        hi += (float)as_h2(f[2])[0] + (float)as_h2(f[2])[1] + (float)as_h2(f[3])[0] + (float)as_h2(f[3])[1];
+      }
+    }
+    corr[t] = -(1032.f * lo + 1152.f * hi);
+  }
+  __syncthreads();
+
+  // A fragment address: rows >= M read the zero entry.
   const bool a_live = mrow < mrows;
+  const int a_base = a_live ? g * mrows + mrow : n_frag;
+  const int a_step = a_live ? 4 * mrows : 0;
+  const int crow0 = (lane >> 4) * 4;  // accumulator rows of this lane
 
   f32x4 acc[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  f16x2 sc[4];  // per-tile scale (s, s) for this lane's column
+  // One batch = one scale group: its MFMAs start from the group's correction
+  // and accumulate the exact products in fp32; the group's scale multiplies
+  // that sum once (per-column scales: the sum is added as is).
+  auto consume = [&](const u32x4(&w)[kSteps], const u32x4& scl, int batch) {
+    const f32x4 cinit =
+        GROUPED ? *reinterpret_cast<const f32x4*>(corr + batch * kMaxM + crow0) : (f32x4){0.f, 0.f, 0.f, 0.f};
+    f32x4 grp[4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) sc[j] = (f16x2){(f16)1.0f, (f16)1.0f};
-
-  // Software pipeline: a batch is one scale group (4 k-steps of 32, 4 KB per
-  // wave); batch b+1 is in flight while batch b is consumed.
-  u32x4 bufA[kPrefetch], bufB[kPrefetch];
-  u32x4 sclA = (u32x4){0, 0, 0, 0}, sclB = (u32x4){0, 0, 0, 0};
-  const uint16_t* ssrc = p.s + chunk * 64 + cc * 8;
-  auto issue = [&](u32x4(&bf)[kPrefetch], u32x4& scl, int kp_first) {
-    if (kp_first < kp1) {
-#pragma unroll
-      for (int d = 0; d < kPrefetch; ++d)
-        bf[d] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(bsrc + (int64_t)(kp_first + d) * 2 * row_words));
-      if (p.grouped) scl = *reinterpret_cast<const u32x4*>(ssrc + (int64_t)(kp_first >> 2) * p.n);
-    }
-  };
-  auto consume = [&](const u32x4(&bf)[kPrefetch], const u32x4& scl, int kp_first) {
-    if (p.grouped) {
+    for (int d = 0; d < kSteps; ++d) {
+      const u32x4 t = afr[a_base + (batch * kSteps + d) * a_step];
+      const f16x8 afrag = __builtin_bit_cast(f16x8, t);
+      const u32x4 own = w[d];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint32_t w = scl[j];
-        const uint32_t h = hsel ? (w >> 16) : (w & 0xffffu);
-        sc[j] = as_h2(h | (h << 16));
+        const uint32_t partner = (uint32_t)__builtin_amdgcn_mov_dpp((int)own[j], 0x128, 0xf, 0xf, false);  // row_ror:8
+        const uint32_t v0 = __builtin_amdgcn_perm(own[j], partner, psel);
+        const uint32_t v1 = v0 >> 8;
+        // grouped: biased values (the group's correction removes the bias);
+        // per-column: the exact fp16 (q - 8), accumulated as the reference does
+        const f16x8 bfrag =
+            GROUPED ? __builtin_bit_cast(f16x8, make_uint4(as_u32(nib_lo_biased(v0, nk)), as_u32(nib_lo_biased(v1, nk)),
+                                                           as_u32(nib_hi_biased(v0, nk)), as_u32(nib_hi_biased(v1, nk))))
+                    : __builtin_bit_cast(f16x8, make_uint4(as_u32(nib_lo_to_h2(v0, nk)), as_u32(nib_lo_to_h2(v1, nk)),
+                                                           as_u32(nib_hi_to_h2(v0, nk)), as_u32(nib_hi_to_h2(v1, nk))));
+        grp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, d == 0 ? cinit : grp[j], 0, 0, 0);
       }
     }
 #pragma unroll
-    for (int d = 0; d < kPrefetch; ++d) {
-      const int kp = kp_first + d;
-      // bounce the coalesced 1 KB through this wave's LDS slot
-      *reinterpret_cast<u32x4*>(&my_stage[lane]) = bf[d];
-      __builtin_amdgcn_wave_barrier();
-      const u32x4 w0 = *reinterpret_cast<const u32x4*>(&my_stage[slot0]);
-      const u32x4 w1 = *reinterpret_cast<const u32x4*>(&my_stage[slot0 + 1]);
-      // A fragment: x rows at k = 32kp + 16prow + 4gq + {0..3} and +8
-      f16x8 afrag = (f16x8){0, 0, 0, 0, 0, 0, 0, 0};
-      if (a_live) {
-        const int kq = ((kp - kp0) << 3) + (prow << 2) + gq;
-        const uint2 lo = xs[kq * mrows + mrow];
-        const uint2 hi = xs[(kq + 2) * mrows + mrow];
-        afrag = __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
-      }
-      const int sh = hsel * 8;
+    for (int j = 0; j < 4; ++j) {
+      if (GROUPED) {
+        const float sc = h2f((uint16_t)(scl[j] >> (16 * hsel)));  // column 16j + 8h + c
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t v0 = w0[j] >> sh;
-        const uint32_t v1 = w1[j] >> sh;
-        f16x2 b0 = nib_lo_to_h2(v0);
-        f16x2 b1 = nib_lo_to_h2(v1);
-        f16x2 b2 = nib_hi_to_h2(v0);
-        f16x2 b3 = nib_hi_to_h2(v1);
-        if (p.grouped) {
-          b0 *= sc[j];
-          b1 *= sc[j];
-          b2 *= sc[j];
-          b3 *= sc[j];
-        }
-        const f16x8 bfrag = __builtin_bit_cast(f16x8, make_uint4(as_u32(b0), as_u32(b1), as_u32(b2), as_u32(b3)));
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, acc[j], 0, 0, 0);
+        for (int i = 0; i < 4; ++i) acc[j][i] += grp[j][i] * sc;
+      } else {
+        acc[j] += grp[j];
       }
-      __builtin_amdgcn_wave_barrier();
     }
   };
 
-  // kp0 and kp1 are multiples of kPrefetch (splits are whole groups)
-  issue(bufA, sclA, kp0);
-  for (int kpb = kp0; kpb < kp1; kpb += 2 * kPrefetch) {
-    issue(bufB, sclB, kpb + kPrefetch);
-    consume(bufA, sclA, kpb);
-    if (kpb + kPrefetch >= kp1) break;
-    issue(bufA, sclA, kpb + 2 * kPrefetch);
-    consume(bufB, sclB, kpb + kPrefetch);
+  // Full rounds re-issue every slot kDepth batches ahead; the tail (fewer than
+  // 2 kDepth batches left) issues only what exists.  Slot i holds batch b + i.
+  // The scheduling barriers keep each re-issue right after the consume that
+  // frees its slot (the scheduler would otherwise sink all loads to the end of
+  // the round and expose a full memory latency per round).
+  int b = 0;
+  for (; b + 2 * kDepth <= nb; b += kDepth) {
+#pragma unroll
+    for (int i = 0; i < kDepth; ++i) {
+      consume(bw[i], bs[i], b + i);
+      __builtin_amdgcn_sched_barrier(0);
+      issue(bw[i], bs[i], b + i + kDepth);
+      __builtin_amdgcn_sched_barrier(0);
+    }
   }
+#pragma unroll
+  for (int i = 0; i < kDepth; ++i) {
+    if (b + i < nb) {
+      consume(bw[i], bs[i], b + i);
+      if (b + i + kDepth < nb) issue(bw[i], bs[i], b + i + kDepth);
+    }
+  }
+#pragma unroll
+  for (int i = 0; i < kDepth - 1; ++i)
+    if (b + kDepth + i < nb) consume(bw[i], bs[i], b + kDepth + i);
 
-  // ---- epilogue ----
-  // acc[j][i] = C[m0 + 4*(lane>>4) + i][chunk*64 + 16j + (lane & 15)]
-  const int crow0 = (lane >> 4) * 4;
-  const int ccol = chunk * 64 + (lane & 15);
-  __shared__ int s_prev;
-  __shared__ uint64_t s_keys[kWaves][kMaxM];
-
-  float final_v[4][4];
-  bool have_final = false;
+  // ---- epilogue: accumulators -> LDS tile [mrows][256] fp32 ----
+  __syncthreads();  // every wave is done with the staged A
+  float* tile = reinterpret_cast<float*>(smem);
+  {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = crow0 + i;
+        if (r < mrows) tile[r * kCols + wave * 64 + 16 * j + (lane & 15)] = acc[j][i];
+      }
+  }
+  __syncthreads();
+  const int n = cg * kCols + tid;  // this thread's output column
+  float v[kMaxM];
+#pragma unroll
+  for (int r = 0; r < kMaxM; ++r) v[r] = r < mrows ? tile[r * kCols + tid] : 0.f;
 
   if (p.splits > 1) {
-    float* part = p.partial + ((int64_t)split * p.m) * p.n;
+    float* part = p.partial + (int64_t)split * p.m * p.n + n;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = crow0 + i;
-        if (r < mrows) part[(int64_t)(m0 + r) * p.n + ccol + 16 * j] = acc[j][i];
-      }
+    for (int r = 0; r < kMaxM; ++r)
+      if (r < mrows) publish(part + (int64_t)r * p.n, v[r]);
+    wait_published();
     __syncthreads();
-    if (tid == 0) s_prev = arrive_release(p.counters + 1 + cg + mb * p.n_cg);
+    int32_t* ctr = p.counters + 1 + cg;
+    if (tid == 0) s_prev = arrive(ctr);
     __syncthreads();
     if (s_prev != p.splits - 1) return;  // not the last split of this tile
-    acquire_device();
-    // the last workgroup sums the partials in split order
+    if (tid == 0) reset_counter(ctr);
+    // Sum the partials in split order; 4 rows x 8 splits of reads in flight.
+    const float* src = p.partial + n;
+    const int64_t split_stride = (int64_t)p.m * p.n;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int r0 = 0; r0 < kMaxM; r0 += 4) {
+      if (r0 < mrows) {
+        float sum[4] = {0.f, 0.f, 0.f, 0.f};
+        for (int s0 = 0; s0 < p.splits; s0 += 8) {
+          float t[4][8];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = crow0 + i;
-        float sum = 0.f;
-        if (r < mrows) {
-          for (int sp = 0; sp < p.splits; ++sp)
-            sum += __builtin_nontemporal_load(p.partial + ((int64_t)sp * p.m + m0 + r) * p.n + ccol + 16 * j);
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int u = 0; u < 8; ++u)
+              t[i][u] = collect(src + (int64_t)min(s0 + u, p.splits - 1) * split_stride +
+                                (int64_t)min(r0 + i, mrows - 1) * p.n);
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+#pragma unroll
+            for (int u = 0; u < 8; ++u) sum[i] += (s0 + u < p.splits) ? t[i][u] : 0.f;
         }
-        final_v[j][i] = sum;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[r0 + i] = sum[i];
       }
-    if (tid == 0) __hip_atomic_store(p.counters + 1 + cg + mb * p.n_cg, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    have_final = true;
-  }
-  if (!have_final) {
-#pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) final_v[j][i] = acc[j][i];
+    }
   }
 
-  // fp16 rounding (and the per-column scale after it, as the reference does)
-  uint16_t outh[4][4];
+  // fp16 rounding (per-column scale after it, as the reference does)
+  f16 colscale = (f16)1.0f;
+  if (!GROUPED) colscale = __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
+  uint16_t outh[kMaxM];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    float colscale = 1.0f;
-    if (!p.grouped) {
-      const int n = ccol + 16 * j;
-      const int base = n & ~31, r = n & 31;
-      const int t = 8 * ((r >> 1) & 3) + ((r >> 3) << 1) + (r & 1);  // inverse of the per-column perm
-      colscale = h2f(p.s[base + t]);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      f16 h = (f16)final_v[j][i];
-      if (!p.grouped) h = h * (f16)colscale;
-      outh[j][i] = __builtin_bit_cast(uint16_t, h);
-    }
+  for (int r = 0; r < kMaxM; ++r) {
+    f16 h = (f16)v[r];
+    if (!GROUPED) h = h * colscale;
+    outh[r] = __builtin_bit_cast(uint16_t, h);
   }
 
   if (EPI == EPI_STORE) {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = crow0 + i;
-        if (r < mrows) p.c[(int64_t)(m0 + r) * p.n + ccol + 16 * j] = outh[j][i];
-      }
+    for (int r = 0; r < kMaxM; ++r)
+      if (r < mrows) p.c[(int64_t)r * p.n + n] = outh[r];
     return;
   }
 
-  // ---- argmax epilogue: per-row max key over this tile, then over tiles ----
+  // ---- argmax: per-row max over this tile's 256 columns, then over tiles ----
 #pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    // rows crow0+i live in lanes with the same lane>>4; reduce over j and lane&15
-    uint64_t best = 0;
-    const int r = crow0 + i;
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (r < mrows) best = max_u64(best, argmax_key(h2f(outh[j][i]), (uint32_t)(ccol + 16 * j)));
+  for (int r = 0; r < kMaxM; ++r) {
+    if (r < mrows) {
+      const uint64_t best = wave_max_u64(argmax_key(h2f(outh[r]), (uint32_t)n));
+      if (lane == 0) s_keys[wave][r] = best;
     }
-    // reduce across the 16 lanes sharing r (xor 1,2,4,8)
-#pragma unroll
-    for (int off = 1; off < 16; off <<= 1) {
-      const uint32_t lo = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane ^ off) & 63) << 2, (int)(uint32_t)best);
-      const uint32_t hi = (uint32_t)__builtin_amdgcn_ds_bpermute(((lane ^ off) & 63) << 2, (int)(uint32_t)(best >> 32));
-      best = max_u64(best, ((uint64_t)hi << 32) | lo);
-    }
-    if ((lane & 15) == 0 && r < kMaxM) s_keys[wave][r] = best;
   }
   __syncthreads();
   if (tid < mrows) {
     uint64_t best = 0;
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) best = max_u64(best, s_keys[w][tid]);
-    p.tile_keys[(int64_t)(m0 + tid) * p.n_cg + cg] = best;
+    publish(p.tile_keys + (int64_t)tid * p.n_cg + cg, best);
   }
+  wait_published();
   __syncthreads();
   int32_t* final_counter = p.counters;
-  if (tid == 0) s_prev = arrive_release(final_counter);
+  if (tid == 0) s_prev = arrive(final_counter);
   __syncthreads();
-  const int total = p.n_cg * ((p.m + kMaxM - 1) / kMaxM);
-  if (s_prev != total - 1) return;
-  acquire_device();
-  for (int r = wave; r < p.m; r += kWaves) {
+  if (s_prev != p.n_cg - 1) return;
+  if (tid == 0) reset_counter(final_counter);
+  for (int r = wave; r < mrows; r += kWaves) {
     uint64_t best = 0;
-    for (int t = lane; t < p.n_cg; t += kWave)
-      best = max_u64(best, __builtin_nontemporal_load(p.tile_keys + (int64_t)r * p.n_cg + t));
+    for (int t = lane; t < p.n_cg; t += kWave) best = max_u64(best, collect(p.tile_keys + (int64_t)r * p.n_cg + t));
     best = wave_max_u64(best);
     if (lane == 0) {
       p.argmax_state[r] = (int64_t)best;
       p.argmax_out[r] = (int64_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
     }
   }
-  if (tid == 0) __hip_atomic_store(final_counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace skinny

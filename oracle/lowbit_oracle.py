@@ -380,6 +380,31 @@ def marlin_gemm(x: np.ndarray, qweight: np.ndarray, scales: np.ndarray, group_si
     return out
 
 
+def marlin_gemm_exact(x: np.ndarray, qweight: np.ndarray, scales: np.ndarray, group_size: int,
+                      rows: np.ndarray | None = None) -> np.ndarray:
+    """The Marlin product without the reference's per-weight rounding.
+
+    ``fp16(sum_k x * (q - 8) * s)`` with every product and sum in float64 (per
+    column scales: as in :func:`marlin_gemm`, applied after the fp16 rounding).
+    This is the mathematical value both :func:`marlin_gemm` (which rounds each
+    ``fp16((q-8)*s)`` first, ``marlin_cuda_kernel.cu:131-159``) and an
+    implementation that scales each group's exact fp32 sum approximate; it
+    equals :func:`marlin_gemm` whenever every ``(q-8)*s`` is representable in
+    fp16 (e.g. power-of-two scales).
+    """
+    a = np.asarray(x, dtype=np.float16)
+    if rows is not None:
+        a = a[np.asarray(rows)]
+    K = a.shape[1]
+    g = _normalize_group(group_size, K)
+    if g == -1:
+        return marlin_gemm(x, qweight, scales, group_size, rows)
+    q = marlin_unpack_codes(qweight).astype(np.float64) - 8.0
+    s = marlin_unpack_scales(scales).astype(np.float64)
+    w = q * s[np.arange(K) // g, :]
+    return (a.astype(np.float64) @ w).astype(np.float16)
+
+
 def silu_f32(v: np.ndarray) -> np.ndarray:
     """``x / (1 + exp(-x))`` in float32 (``marlin_cuda_kernel.cu:205-207``)."""
     v = np.asarray(v, dtype=np.float32)

@@ -239,6 +239,25 @@ def test_marlin_gemm_one_hot_and_c_restatement(group):
         assert np.array_equal(ref.astype(np.float16), y_np)
 
 
+def test_marlin_gemm_exact_pins():
+    """The exact-scale product: equal to the natural-layout float64 product,
+    and to the reference rounding wherever (q-8)*s is exact in fp16."""
+    K, N = 512, 256
+    codes, qw, s_nat, s_perm, x = O.make_marlin_inputs(4, K, N, 128, seed=21)
+    got = O.marlin_gemm_exact(x, qw, s_perm, 128)
+    natural = x.astype(np.float64) @ ((codes.astype(np.float64) - 8) * s_nat.astype(np.float64)[np.arange(K) // 128])
+    assert np.array_equal(got.view(np.uint16), natural.astype(np.float16).view(np.uint16))
+    # power-of-two scales: every fp16 (q-8)*s is exact, so both rounding orders agree
+    rng = np.random.default_rng(22)
+    s2 = (2.0 ** rng.integers(-8, -2, size=s_nat.shape)).astype(np.float16)
+    s2_perm = O.marlin_pack_scales(s2, per_column=False)
+    assert np.array_equal(O.marlin_gemm_exact(x, qw, s2_perm, 128).view(np.uint16),
+                          O.marlin_gemm(x, qw, s2_perm, 128).view(np.uint16))
+    # general scales: the two differ only by the per-weight rounding noise
+    ref = O.marlin_gemm(x, qw, s_perm, 128).astype(np.float64)
+    assert np.abs(got.astype(np.float64) - ref).max() < 1e-2
+
+
 def test_silu_closed_form():
     g = np.array([[0.0, 1.0, -1.0, 4.0, -10.0, 0.5]], dtype=np.float16)
     u = np.array([[1.0, 2.0, 3.0, 0.5, 1.0, -2.0]], dtype=np.float16)
