@@ -119,11 +119,17 @@ def sets_for(bytes_per_set, minimum=8):
     return max(minimum, math.ceil(2.0 * MALL_BYTES / bytes_per_set))
 
 
-def cpu_baseline(m, k, n):
-    """CPU restatement of the dequantise-then-matmul reference path on the headline
-    shape (oracle package; the reference raises for Marlin on CPU, ops.py:65-79)."""
-    import numpy as np
+def _cpu_threads():
     from threadpoolctl import threadpool_info
+
+    return max([t.get("num_threads", 1) for t in threadpool_info()] + [1])
+
+
+def cpu_baseline(m, k, n, budget_s=12.0):
+    """CPU restatement of the dequantise-then-matmul reference path on the headline
+    shape (oracle package; the reference itself raises for Marlin on CPU,
+    ops.py:65-79), timed for about `budget_s` seconds."""
+    import numpy as np
 
     from oracle import lowbit_oracle as O
 
@@ -133,22 +139,83 @@ def cpu_baseline(m, k, n):
     x = rng.normal(0, 1, (m, k)).astype(np.float16)
     O.marlin_gemm(x, qw, s, 128)  # warm-up
     times = []
-    t_end = time.perf_counter() + 15.0
-    while len(times) < 3 and (not times or time.perf_counter() < t_end):
+    t_end = time.perf_counter() + budget_s
+    while len(times) < 3 or time.perf_counter() < t_end:
         t0 = time.perf_counter()
         O.marlin_gemm(x, qw, s, 128)
         times.append(time.perf_counter() - t0)
     sec = sum(times) / len(times)
-    threads = max([t.get("num_threads", 1) for t in threadpool_info()] + [1])
+    threads = _cpu_threads()
     return {
         "value": round(marlin_bytes(m, k, n) / sec / 1e9, 4),
         "unit": "GB/s",
         "cores": int(threads),
         "kind": "port",
-        "sample": f"{len(times)} full calls of M={m} K={k} N={n} g128 (numpy unpack + fp16 dequant single-threaded, "
-                  f"float64 matmul on {threads} BLAS threads); {sec * 1e3:.0f} ms/call",
+        "sample": f"{len(times)} full calls of the headline M={m} K={k} N={n} g128 in {sum(times):.1f} s "
+                  f"(numpy unpack + fp16 dequant single-threaded, float64 matmul on {threads} BLAS threads); "
+                  f"{sec * 1e3:.0f} ms/call",
         "cpu": platform.processor() or platform.machine(),
     }
+
+
+def cpu_rowwise_cfg1(budget_s=4.0):
+    """the reference's CPU rowwise 4-bit GEMV (loader.py:427-465,
+    ops.py:16-44) restated in numpy, x [1,4096], W [4096,4096] g128: (a) dequant +
+    matmul per call, (b) matmul on pre-dequantised weights."""
+    import numpy as np
+
+    from oracle import lowbit_oracle as O
+
+    _, packed, scales, x = O.make_rowwise_inputs(4096, 4096, 4, 128, batch=1, seed=0)
+    nbytes = rowwise_bytes(1, 4096, 4096, 4, 128)
+
+    def timed(fn):
+        fn()
+        ts, t_end = [], time.perf_counter() + budget_s / 2
+        while len(ts) < 3 or time.perf_counter() < t_end:
+            t0 = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t0)
+        return sum(ts) / len(ts), len(ts)
+
+    sec_a, na = timed(lambda: O.rowwise_gemv(packed, scales, x[0], 4096, 128, 4))
+    w = O.rowwise_dequant_f32(packed, scales, 4096, 128, 4)
+    xf = x[0].astype(np.float32)
+    sec_b, nb = timed(lambda: (w @ xf).astype(np.float16))
+    return {"dequant_matmul": {"us_per_call": round(sec_a * 1e6, 1), "GB/s": round(nbytes / sec_a / 1e9, 4), "calls": na},
+            "matmul_only_predequantised": {"us_per_call": round(sec_b * 1e6, 1), "GB/s": round(nbytes / sec_b / 1e9, 4),
+                                           "calls": nb},
+            "cores": int(_cpu_threads()), "kind": "port"}
+
+
+def read_traffic(path):
+    """HBM bytes per headline launch from the committed counter summary, if any."""
+    try:
+        with open(path) as f:
+            for line in f:
+                if line.startswith("traffic_bytes_per_launch:"):
+                    return float(line.split(":", 1)[1])
+    except OSError:
+        pass
+    return None
+
+
+def pmc_probe(torch, lc, dev, calls=24):
+    """Eager headline calls plus a plain elementwise copy of known size, for the
+    FETCH_SIZE / WRITE_SIZE counter runs (the copy calibrates the counters)."""
+    m, k, n = 1, 5120, 17408
+    ns = sets_for(marlin_bytes(m, k, n))
+    prob = MarlinProblem(torch, dev, m, k, n, ns, seed=1)
+    torch.cuda.synchronize()
+    for i in range(calls):
+        prob.call(lc, i % ns)
+    torch.cuda.synchronize()
+    src = torch.ones((128 * 2 ** 20,), dtype=torch.float16, device=dev)  # 256 MiB read, 256 MiB written
+    dst = torch.empty_like(src)
+    for _ in range(4):
+        torch.add(src, 0, out=dst)
+    torch.cuda.synchronize()
+    log(f"[pmc-probe] {calls} headline calls, 4 copies of 256 MiB")
 
 
 def main():
@@ -160,6 +227,7 @@ def main():
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
+    ap.add_argument("--pmc-probe", action="store_true", help="run the counter-calibration probe and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -176,6 +244,9 @@ def main():
         sys.exit(1)
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.pmc_probe:
+        pmc_probe(torch, lc, dev)
+        return
     use_graph = not args.no_graph
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; graph={use_graph}")
 
@@ -210,7 +281,9 @@ def main():
                                + (", hipGraph replay" if use_graph else ", eager launches"),
                    "m": m, "k": k, "n": n, "group_size": 128, "weight_sets": n_sets},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(gbs / HBM_PEAK_GBS, 4), "traffic": None,
+                     "frac": round(gbs / HBM_PEAK_GBS, 4),
+                     "traffic": read_traffic(os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                                                          "marlin_gemv_m1_k5120_n17408_traffic.txt")),
                      "bytes_per_launch": per_call, "us_per_launch": round(us_per, 3)},
     }
 
@@ -261,6 +334,7 @@ def main():
     if not args.skip_cpu:
         try:
             result["cpu_baseline"] = cpu_baseline(m, k, n)
+            result["cpu_baseline"]["cfg1_rowwise_reference_cpu_path"] = cpu_rowwise_cfg1()
         except Exception as exc:  # the baseline is reported, never required
             result["cpu_baseline"] = {"value": None, "unit": "GB/s", "cores": 0, "kind": "port",
                                       "sample": f"failed: {exc}"}

@@ -104,7 +104,11 @@ int lb_lowbit_row_dequant(const uint8_t* qweight, int64_t rows, int64_t packed_c
 /* Bytes of scratch the Marlin entry points need for this problem. */
 size_t lb_marlin_scratch_bytes(int64_t prob_m, int64_t prob_n, int64_t prob_k, int64_t groupsize);
 
-/* C[M, N] = A[M, K] @ dequant(B), fp16 weights, fp32 accumulate, fp16 C.
+/* C[M, N] = A[M, K] @ dequant(B), fp32 accumulate, fp16 C.  Grouped scales:
+ * for M <= 16 each group's fp32 sum of x * (q - 8) is multiplied by the scale
+ * once; for M > 16 the fp16 weights fp16((q - 8) * s) are accumulated, as the
+ * reference does for every M.  Per-column scales: fp16(sum) * s, as the
+ * reference.  Both stay within the reference tolerance.
  * Replaces marlin_cuda (csrc/marlin_cuda_kernel.cu:917-1005) as called by
  * run_lowbit_marlin_gemm (csrc/langburst_ext.cpp:67-114). */
 int lb_marlin_gemm(const uint16_t* A, const int32_t* B, uint16_t* C, const uint16_t* s,

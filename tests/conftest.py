@@ -30,6 +30,17 @@ def gpu_available() -> bool:
 
 
 @pytest.fixture(scope="session")
+def built():
+    """The compiled library and module; built in place when a fresh checkout lacks them."""
+    import neurova_amd
+    from neurova_amd import build as nb
+
+    if not (neurova_amd.library_path().exists() and neurova_amd.extension_path().exists()):
+        nb.build()
+    return True
+
+
+@pytest.fixture(scope="session")
 def dev():
     """cuda:0 with the built extension; fails loudly (not skips) when a GPU is present but the build is missing."""
     import torch
