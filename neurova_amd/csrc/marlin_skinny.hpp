@@ -232,7 +232,10 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   stage_load(0);
   __builtin_amdgcn_sched_barrier(0);  // staging loads strictly before the weight loads
 #pragma unroll
-  for (int i = 0; i < kDepth; ++i) issue(bw[i], bs[i], min(i, nb - 1));
+  for (int i = 0; i < kDepth; ++i) {
+    issue(bw[i], bs[i], min(i, nb - 1));
+    __builtin_amdgcn_sched_barrier(0);  // keep slot order: the loop's waits assume it
+  }
   __builtin_amdgcn_sched_barrier(0);
   stage_store(0);
   for (int base = kThreads * kStageUnroll; base < items; base += kThreads * kStageUnroll) {
