@@ -213,7 +213,11 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
     pl.lds = std::max(stage, (size_t)m * skinny::kCols * 4);
   } else {
     pl.skinny = false;
-    pl.mb = m > 64 ? 8 : (m > 32 ? 4 : 2);
+#ifdef LB_GEMM_MB
+    pl.mb = LB_GEMM_MB;
+#else
+    pl.mb = m > 32 ? 4 : 2;  // MB = 8 does not fit two workgroups per CU in registers
+#endif
     const int64_t bm = 16 * pl.mb;
     pl.n_mb = (int)((m + bm - 1) / bm);
     const int64_t tiles = (int64_t)pl.n_cg * pl.n_mb;
@@ -263,6 +267,9 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   if (var == V_ARGMAX ? (!argmax_state || !argmax_out) : !c) return LB_ERR_ARG;
   if (!lbh::aligned(a, 16) || !lbh::aligned(b, 16) || !lbh::aligned(s, 16) || (c && !lbh::aligned(c, 2)))
     return LB_ERR_ALIGN;
+  // The GEMM kernel addresses A, B and s through 32-bit buffer resources.
+  const int64_t a_bytes = m * k * 2 * (var == V_SILU ? 2 : 1);
+  if (m > skinny::kMaxM && (a_bytes >= (1LL << 31) || k * n / 2 >= (1LL << 31))) return LB_ERR_PROB_SHAPE;
   const Plan pl = make_plan(m, n, k, workspace_len);
   if (workspace_len < counters_needed(pl, var == V_ARGMAX)) return LB_ERR_WORKSPACE;
   const size_t need = pl.partial_bytes + (var == V_ARGMAX ? pl.keys_bytes : 0);
@@ -298,17 +305,24 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   p.m = (int)m; p.n = (int)n; p.k = (int)k; p.grouped = grouped; p.splits = pl.splits;
   p.kp_total = (int)(k / 32); p.n_cg = pl.n_cg; p.n_mb = pl.n_mb;
   dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, (unsigned)pl.n_mb);
-#define LB_GM(MBV, AMV, EPV) hipLaunchKernelGGL((gemm::marlin_gemm_kernel<MBV, AMV, EPV>), grid, dim3(gemm::kThreads), 0, st, p)
-#define LB_GM_MB(AMV, EPV)               \
-  do {                                   \
-    if (pl.mb == 8) LB_GM(8, AMV, EPV);  \
-    else if (pl.mb == 4) LB_GM(4, AMV, EPV); \
-    else LB_GM(2, AMV, EPV);             \
+#define LB_GM(MBV, AMV, EPV, GV) \
+  hipLaunchKernelGGL((gemm::marlin_gemm_kernel<MBV, AMV, EPV, GV>), grid, dim3(gemm::kThreads), 0, st, p)
+#define LB_GM_G(MBV, AMV, EPV)                      \
+  do {                                              \
+    if (grouped) LB_GM(MBV, AMV, EPV, true);        \
+    else LB_GM(MBV, AMV, EPV, false);               \
+  } while (0)
+#define LB_GM_MB(AMV, EPV)                      \
+  do {                                          \
+    if (pl.mb == 8) LB_GM_G(8, AMV, EPV);       \
+    else if (pl.mb == 4) LB_GM_G(4, AMV, EPV);  \
+    else LB_GM_G(2, AMV, EPV);                  \
   } while (0)
   if (var == V_PLAIN) LB_GM_MB(gemm::A_PLAIN, gemm::EPI_STORE);
   else if (var == V_SILU) LB_GM_MB(gemm::A_SILU_PACKED, gemm::EPI_STORE);
   else LB_GM_MB(gemm::A_PLAIN, gemm::EPI_ARGMAX);
 #undef LB_GM_MB
+#undef LB_GM_G
 #undef LB_GM
   return lbh::launch_status();
 }

@@ -1,24 +1,30 @@
 // Marlin-layout W4A16 GEMM for prefill batches (M > 16) on gfx950.
 //
-// Same fragment construction as the decode kernel (lb_marlin_skinny.hip):
-// B fragments of v_mfma_f32_16x16x32_f16 are built in registers from the
+// Same fragment construction as the decode kernel (marlin_skinny.hpp): B
+// fragments of v_mfma_f32_16x16x32_f16 are built in registers from the
 // reference's Marlin layout (langburst/csrc/marlin_cuda_kernel.cu; packing in
-// adapters/qwen36_tools/quantize.py:180-243), exact fp16 (q-8) times the fp16
-// group scale.  Here each dequantised B fragment feeds MB MFMAs (MB 16-row
-// blocks of A), so the VALU dequant cost is amortised over 16*MB rows.
+// adapters/qwen36_tools/quantize.py:180-243) -- one 16-byte slot per lane, the
+// pair's other slot from lane ^ 8 by DPP -- as the exact fp16 (q-8) times the
+// fp16 group scale (the reference's __hmul2 rounding).  Each dequantised B
+// fragment feeds MB MFMAs (MB 16-row blocks of A), so the VALU dequant cost is
+// amortised over 16*MB rows.
 //
 // Workgroup tile: (16*MB rows) x 256 columns; wave w owns 64-column chunk w.
-// Per 32-k step:
-//   A  -- global rows (64 B each) -> registers -> LDS, rearranged so that the
-//         A fragment of lane (g, m) is 16 contiguous bytes: frag[g][m] =
-//         x[m][16p + 4g' + {0..3}] ++ x[m][16p + 4g' + 8 + {0..3}], g = 2p+g'.
-//         Double-buffered, one __syncthreads per step.
-//   B  -- each lane loads the two adjacent 16-byte slots its fragment needs
-//         (slots 4c+2g', 4c+2g'+1 of row p) straight from global memory.
-// Optional split-K over S workgroups with the same deterministic fixup as the
-// decode kernel (fp32 partials in scratch, last arrival sums in split order).
+// The k loop runs in stages of one scale group (128 k = 4 MFMA steps):
+//   A  -- the stage's rows are read from global memory (16 B per item, one
+//         row's 256 bytes by 16 consecutive threads) one stage ahead into
+//         registers, then written to a double-buffered LDS tile in fragment
+//         order (entry (d, g, r) = A[r][32d + 16(g>>1) + 4(g&1) + {0..3}] ++
+//         the same + 8); one __syncthreads per stage.
+//   B  -- each lane's slots and the group scales two stages ahead.
+// The stage loop is unrolled by two so that buffer and slot indices are
+// compile-time constants.  Optional split-K over S workgroups uses the same
+// deterministic hand-off as the decode kernel (fp32 partials in scratch, the
+// last arrival sums them in split order).
 
 #pragma once
+#include <type_traits>
+
 #include "lb_common.hpp"
 
 namespace lb {
@@ -70,55 +76,23 @@ __device__ __forceinline__ void split_range(const Params& p, int split, int& kp0
   kp1 = g1 << 2;
 }
 
-// Loads the 32 halves (64 B) of A row `r`, k-step kp, half p (k 16p..16p+15)
-// and returns the two fragment quads (g = 2p, g = 2p+1) as 2 x 16 bytes.
-template <int AM>
-__device__ __forceinline__ void load_a_half(const Params& p, int r, int kp, int ph, uint4& f0, uint4& f1) {
-  if (r >= p.m) {
-    f0 = make_uint4(0, 0, 0, 0);
-    f1 = make_uint4(0, 0, 0, 0);
-    return;
-  }
-  const int kk = kp * 32 + ph * 16;
-  uint4 v0, v1;  // k kk..kk+7, kk+8..kk+15
-  if (AM == A_PLAIN) {
-    const uint4* src = reinterpret_cast<const uint4*>(p.a + (int64_t)r * p.k + kk);
-    v0 = src[0];
-    v1 = src[1];
-  } else {
-    const uint16_t* row = p.a + (int64_t)r * (2 * (int64_t)p.k);
-    const uint4* gs = reinterpret_cast<const uint4*>(row + kk);
-    const uint4* us = reinterpret_cast<const uint4*>(row + p.k + kk);
-    uint4 gv[2] = {gs[0], gs[1]};
-    uint4 uv[2] = {us[0], us[1]};
-    uint4 ov[2];
-#pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      const uint32_t gw[4] = {gv[t].x, gv[t].y, gv[t].z, gv[t].w};
-      const uint32_t uw[4] = {uv[t].x, uv[t].y, uv[t].z, uv[t].w};
-      uint32_t o[4];
-#pragma unroll
-      for (int w = 0; w < 4; ++w) {
-        const float g0 = h2f((uint16_t)(gw[w] & 0xffffu)), g1 = h2f((uint16_t)(gw[w] >> 16));
-        const float u0 = h2f((uint16_t)(uw[w] & 0xffffu)), u1 = h2f((uint16_t)(uw[w] >> 16));
-        o[w] = (uint32_t)f2h(silu(g0) * u0) | ((uint32_t)f2h(silu(g1) * u1) << 16);
-      }
-      ov[t] = make_uint4(o[0], o[1], o[2], o[3]);
-    }
-    v0 = ov[0];
-    v1 = ov[1];
-  }
-  // quads: v0 = (q0, q1), v1 = (q2, q3) where quad qd = k kk+4qd..+3
-  // fragment g=2p   : quads 0 and 2 ; fragment g=2p+1 : quads 1 and 3
-  f0 = make_uint4(v0.x, v0.y, v1.x, v1.y);
-  f1 = make_uint4(v0.z, v0.w, v1.z, v1.w);
+// Raw buffer resource (gfx9 V#: stride 0, 32-bit data format).  Loads at or
+// past num_records return zero: rows of the last M block beyond M use that.
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
 }
 
-template <int MB, int AM, int EPI>
+constexpr int kSteps = 4;  // 32-k steps per stage (one scale group of 128)
+
+template <int MB, int AM, int EPI, bool GROUPED>
 __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
   constexpr int BM = 16 * MB;
-  // A fragments: [2 buffers][4 g][BM rows] x 16 B
-  __shared__ __attribute__((aligned(16))) uint4 afr[2][4][BM];
+  // A stage in LDS, fragment order, double-buffered: entry (d, g, r) is 16 B:
+  // A[r][32d + 16(g>>1) + 4(g&1) + {0..3}] ++ the same + 8.  Each (d, g) block
+  // is padded by one entry so that the staging writes of one row, which go to
+  // different (d, g) blocks, land in different banks.
+  constexpr int kBlk = BM + 1;
+  __shared__ __attribute__((aligned(16))) uint4 afr[2][kSteps * 4 * kBlk];
   __shared__ int s_prev;
   __shared__ uint64_t s_keys[kWaves][BM];
 
@@ -132,111 +106,148 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
 
   int kp0, kp1;
   split_range(p, split, kp0, kp1);
+  const int st0 = kp0 / kSteps;         // first scale group (stage)
+  const int nst = (kp1 - kp0) / kSteps; // stages of this split
 
   const int chunk = cg * kWaves + wave;
-  const int64_t row_words = 2 * (int64_t)p.n;
+  const uint32_t row_bytes = 8u * (uint32_t)p.n;
   const int g = lane >> 4;
   const int hsel = (lane >> 3) & 1;
   const int cc = lane & 7;
   const int prow = g >> 1;
   const int gq = g & 1;
-  // B fragment source: slots 4cc + 2gq and +1 of row 2kp + prow of this chunk
-  const uint32_t* bsrc = p.b + (int64_t)prow * row_words + (int64_t)chunk * 128 + (cc * 4 + gq * 2) * 4;
-  const uint16_t* ssrc = p.s + chunk * 64 + cc * 8;
+  const __amdgpu_buffer_rsrc_t rb = buffer_of(p.b, (uint32_t)p.k / 16u * row_bytes);
+  const __amdgpu_buffer_rsrc_t rs = buffer_of(p.s, (GROUPED ? (uint32_t)(p.k / 128) : 1u) * (uint32_t)p.n * 2u);
+  // each lane loads slot 4c + 2gq + h of row 2kp + prow; the pair's other slot
+  // comes from lane ^ 8 (DPP row rotation)
+  const uint32_t b_off = (uint32_t)prow * row_bytes + (uint32_t)chunk * 512u + (uint32_t)(cc * 4 + gq * 2 + hsel) * 16u;
+  const uint32_t s_off = ((uint32_t)chunk * 64u + (uint32_t)cc * 8u) * 2u;
+  const uint32_t psel = hsel ? 0x07030501u : 0x02060004u;
   const NibConsts nk = nib_consts();
 
-  // A staging assignment: (row, half) pairs, BM*2 of them over 256 threads
-  constexpr int kAItems = BM * 2;
-  constexpr int kAPerThread = (kAItems + kThreads - 1) / kThreads;
+  // ---- A staging: items (row r, octet o) of 8 halves, r-major so that 16
+  // consecutive threads read one row's 256 contiguous bytes ----
+  constexpr int kAItems = BM * 16;
+  constexpr int kAPer = kAItems / kThreads;
+  static_assert(kAItems % kThreads == 0, "A staging items");
+  const int64_t a_row_halves = AM == A_SILU_PACKED ? 2 * (int64_t)p.k : (int64_t)p.k;
+  const __amdgpu_buffer_rsrc_t ra = buffer_of(p.a, (uint32_t)((int64_t)p.m * a_row_halves * 2));
+  uint4 areg[kAPer];
+  uint4 ureg[AM == A_SILU_PACKED ? kAPer : 1];
+  auto load_a = [&](int stage) {
+#pragma unroll
+    for (int t = 0; t < kAPer; ++t) {
+      const int item = tid + t * kThreads;
+      const int r = item >> 4, o = item & 15;
+      const uint32_t off = (uint32_t)(((int64_t)(m0 + r) * a_row_halves + (int64_t)stage * 128 + 8 * o) * 2);
+      areg[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, off, 0, 0));
+      if (AM == A_SILU_PACKED)
+        ureg[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, off + 2u * (uint32_t)p.k, 0, 0));
+    }
+  };
+  auto store_a = [&](int buf) {
+#pragma unroll
+    for (int t = 0; t < kAPer; ++t) {
+      const int item = tid + t * kThreads;
+      const int r = item >> 4, o = item & 15;
+      uint4 w = areg[t];
+      if (AM == A_SILU_PACKED) {
+        const uint4 u = ureg[t];
+        const uint32_t gw[4] = {w.x, w.y, w.z, w.w};
+        const uint32_t uw[4] = {u.x, u.y, u.z, u.w};
+        uint32_t ov[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float g0 = h2f((uint16_t)(gw[e] & 0xffffu)), g1 = h2f((uint16_t)(gw[e] >> 16));
+          const float u0 = h2f((uint16_t)(uw[e] & 0xffffu)), u1 = h2f((uint16_t)(uw[e] >> 16));
+          ov[e] = (uint32_t)f2h(silu(g0) * u0) | ((uint32_t)f2h(silu(g1) * u1) << 16);
+        }
+        w = make_uint4(ov[0], ov[1], ov[2], ov[3]);
+      }
+      // octet o = 4d + 2prow + half: halves 0..3 -> (d, g = 2prow), 4..7 -> (d, g = 2prow + 1)
+      const int d = o >> 2, pr = (o >> 1) & 1, half = o & 1;
+      uint2* dst0 = reinterpret_cast<uint2*>(&afr[buf][(d * 4 + 2 * pr) * kBlk + r]) + half;
+      uint2* dst1 = reinterpret_cast<uint2*>(&afr[buf][(d * 4 + 2 * pr + 1) * kBlk + r]) + half;
+      *dst0 = make_uint2(w.x, w.y);
+      *dst1 = make_uint2(w.z, w.w);
+    }
+  };
+
+  // ---- B ring: two stages of (4 slots + the group's scales) per lane ----
+  u32x4 bst[2][kSteps];
+  u32x4 sst[2];
+  auto load_b = [&](int slot, int stage) {
+#pragma unroll
+    for (int d = 0; d < kSteps; ++d)
+      bst[slot][d] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, b_off, (uint32_t)(stage * 8 + 2 * d) * row_bytes, 0));
+    if (GROUPED)
+      sst[slot] = __builtin_bit_cast(
+          u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, s_off, (uint32_t)stage * (uint32_t)p.n * 2u, 0));
+  };
 
   f32x4 acc[4][MB];
 #pragma unroll
   for (int j = 0; j < 4; ++j)
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[j][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
-  f16x2 sc[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) sc[j] = (f16x2){(f16)1.0f, (f16)1.0f};
 
-  uint4 areg[kAPerThread][2];
-  auto load_a = [&](int kp) {
-#pragma unroll
-    for (int t = 0; t < kAPerThread; ++t) {
-      const int item = tid + t * kThreads;
-      if (item < kAItems) load_a_half<AM>(p, m0 + (item >> 1), kp, item & 1, areg[t][0], areg[t][1]);
-    }
-  };
-  auto store_a = [&](int buf) {
-#pragma unroll
-    for (int t = 0; t < kAPerThread; ++t) {
-      const int item = tid + t * kThreads;
-      if (item < kAItems) {
-        const int r = item >> 1, ph = item & 1;
-        afr[buf][2 * ph][r] = areg[t][0];
-        afr[buf][2 * ph + 1][r] = areg[t][1];
-      }
-    }
-  };
-
-  u32x4 bcur0, bcur1, bnext0, bnext1;
-  auto load_b = [&](int kp, u32x4& b0, u32x4& b1) {
-    const u32x4* src = reinterpret_cast<const u32x4*>(bsrc + (int64_t)kp * 2 * row_words);
-    b0 = __builtin_nontemporal_load(src);
-    b1 = __builtin_nontemporal_load(src + 1);
-  };
-
-  if (kp0 < kp1) {
-    load_a(kp0);
-    load_b(kp0, bcur0, bcur1);
-    store_a(0);
-  }
-  __syncthreads();
-
-  int buf = 0;
-  for (int kp = kp0; kp < kp1; ++kp) {
-    const bool more = kp + 1 < kp1;
-    if (more) {
-      load_a(kp + 1);
-      load_b(kp + 1, bnext0, bnext1);
-    }
-    if (p.grouped && (kp & 3) == 0) {
-      const u32x4 sv = *reinterpret_cast<const u32x4*>(ssrc + (int64_t)(kp >> 2) * p.n);
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t w = sv[j];
-        const uint32_t h = hsel ? (w >> 16) : (w & 0xffffu);
-        sc[j] = as_h2(h | (h << 16));
-      }
-    }
-    f16x8 afrag[MB];
-#pragma unroll
-    for (int i = 0; i < MB; ++i) afrag[i] = __builtin_bit_cast(f16x8, afr[buf][g][i * 16 + (lane & 15)]);
-    const int sh = hsel * 8;
+  auto compute = [&](int buf, int slot) {
+    f16x2 sc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const uint32_t v0 = bcur0[j] >> sh;
-      const uint32_t v1 = bcur1[j] >> sh;
-      f16x2 b0 = nib_lo_to_h2(v0, nk);
-      f16x2 b1 = nib_lo_to_h2(v1, nk);
-      f16x2 b2 = nib_hi_to_h2(v0, nk);
-      f16x2 b3 = nib_hi_to_h2(v1, nk);
-      if (p.grouped) {
-        b0 *= sc[j];
-        b1 *= sc[j];
-        b2 *= sc[j];
-        b3 *= sc[j];
-      }
-      const f16x8 bfrag = __builtin_bit_cast(f16x8, make_uint4(as_u32(b0), as_u32(b1), as_u32(b2), as_u32(b3)));
+      const uint32_t h = GROUPED ? ((sst[slot][j] >> (16 * hsel)) & 0xffffu) : 0x3c00u;  // fp16 1.0
+      sc[j] = as_h2(h | (h << 16));
+    }
 #pragma unroll
-      for (int i = 0; i < MB; ++i) acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag[i], bfrag, acc[j][i], 0, 0, 0);
+    for (int d = 0; d < kSteps; ++d) {
+      f16x8 bfrag[4];
+      const u32x4 own = bst[slot][d];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint32_t partner = (uint32_t)__builtin_amdgcn_mov_dpp((int)own[j], 0x128, 0xf, 0xf, false);  // row_ror:8
+        const uint32_t v0 = __builtin_amdgcn_perm(own[j], partner, psel);
+        const uint32_t v1 = v0 >> 8;
+        // exact fp16 (q - 8) times the fp16 group scale: the rounding of the reference's __hmul2
+        const f16x2 b0 = nib_lo_to_h2(v0, nk) * sc[j];
+        const f16x2 b1 = nib_lo_to_h2(v1, nk) * sc[j];
+        const f16x2 b2 = nib_hi_to_h2(v0, nk) * sc[j];
+        const f16x2 b3 = nib_hi_to_h2(v1, nk) * sc[j];
+        bfrag[j] = __builtin_bit_cast(f16x8, make_uint4(as_u32(b0), as_u32(b1), as_u32(b2), as_u32(b3)));
+      }
+      const uint4* abase = &afr[buf][(d * 4 + g) * kBlk + (lane & 15)];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        const f16x8 afrag = __builtin_bit_cast(f16x8, abase[16 * i]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag[j], acc[j][i], 0, 0, 0);
+      }
     }
-    if (more) {
-      store_a(buf ^ 1);
-      bcur0 = bnext0;
-      bcur1 = bnext1;
-    }
+  };
+
+  // ---- pipeline: A one stage ahead (registers -> LDS), B two stages ahead ----
+  if (nst > 0) {
+    load_a(st0);
+    load_b(0, st0);
+    if (nst > 1) load_b(1, st0 + 1);
+    store_a(0);
     __syncthreads();
-    buf ^= 1;
+    if (nst > 1) load_a(st0 + 1);
+    // Stage s uses LDS buffer and B slot s & 1; unrolled by two so that both
+    // are compile-time constants (no indexed register access).
+    auto stage = [&](int s, auto par) {
+      constexpr int c = decltype(par)::value;
+      compute(c, c);
+      if (s + 2 < nst) load_b(c, st0 + s + 2);
+      if (s + 1 < nst) store_a(c ^ 1);  // buffer c ^ 1 was last read in stage s - 1
+      __syncthreads();
+      if (s + 2 < nst) load_a(st0 + s + 2);
+    };
+    for (int s = 0; s < nst; s += 2) {
+      stage(s, std::integral_constant<int, 0>{});
+      if (s + 1 >= nst) break;
+      stage(s + 1, std::integral_constant<int, 1>{});
+    }
   }
 
   // ---- epilogue ----
@@ -279,7 +290,7 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
   }
 
   float colscale[4] = {1.f, 1.f, 1.f, 1.f};
-  if (!p.grouped) {
+  if (!GROUPED) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const int n = ccol + 16 * j;
@@ -297,7 +308,7 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
         for (int e = 0; e < 4; ++e) {
           const int r = rbase + 16 * i + e;
           f16 h = (f16)acc[j][i][e];
-          if (!p.grouped) h = h * (f16)colscale[j];
+          if (!GROUPED) h = h * (f16)colscale[j];
           if (r < p.m) p.c[(int64_t)r * p.n + ccol + 16 * j] = __builtin_bit_cast(uint16_t, h);
         }
     return;
@@ -313,7 +324,7 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         f16 h = (f16)acc[j][i][e];
-        if (!p.grouped) h = h * (f16)colscale[j];
+        if (!GROUPED) h = h * (f16)colscale[j];
         best = max_u64(best, argmax_key((float)h, (uint32_t)(ccol + 16 * j)));
       }
 #pragma unroll
