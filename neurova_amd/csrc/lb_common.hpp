@@ -113,6 +113,17 @@ __device__ __forceinline__ uint64_t collect(const uint64_t* p) {
   return __hip_atomic_load(const_cast<uint64_t*>(p), __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// The same device-coherent (sc1) stores and loads, sixteen bytes at a time
+// through a buffer resource (cache-policy operand 16 = sc1 on gfx950), for
+// hand-offs of whole accumulator registers.
+constexpr int kSc1 = 16;
+__device__ __forceinline__ void publish16(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
+  __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kSc1);
+}
+__device__ __forceinline__ f32x4 collect16(__amdgpu_buffer_rsrc_t r, uint32_t off) {
+  return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1));
+}
+
 // Waits until every vector-memory operation this thread issued (loads,
 // stores, atomics) has been acknowledged; the memory clobber keeps the
 // compiler from moving memory accesses across it.

@@ -156,7 +156,11 @@ struct Plan {
   int mb = 1;        // GEMM: 16-row blocks per workgroup
   int n_mb = 1;
   int n_cg = 0;
-  int splits = 1;
+  int splits = 1;    // decode: K splits of every column tile
+  int full_tiles = 0;   // GEMM: tiles computed whole
+  int tail_tiles = 0;   // GEMM: tiles split over K ...
+  int tail_splits = 1;  // ... this many ways
+  int64_t wgs = 0;      // GEMM workgroups
   size_t lds = 0;    // decode kernel dynamic LDS
   size_t x_bytes = 0; // decode kernel: staged activations
   size_t partial_bytes = 0;
@@ -166,11 +170,8 @@ struct Plan {
 #ifndef LB_SKINNY_WGS_PER_CU
 #define LB_SKINNY_WGS_PER_CU 2    // decode workgroups resident per CU (register-limited)
 #endif
-#ifndef LB_GEMM_TARGET_WGS
-#define LB_GEMM_TARGET_WGS 512    // two workgroups per CU
-#endif
 constexpr int kSkinnyWGsPerCU = LB_SKINNY_WGS_PER_CU;
-constexpr int kGemmTargetWGs = LB_GEMM_TARGET_WGS;
+constexpr int kGemmMaxTailSplits = 16;
 constexpr size_t kSkinnyMaxX = 48 * 1024;
 
 // Compute units of the current device (cached per device; 256 on a full MI355X,
@@ -187,7 +188,26 @@ inline int device_cus() {
   return v;
 }
 
-inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
+// GEMM tail split: the tiles left after the last full round of resident
+// workgroups are split over K.  S minimises the tail's length in tile times,
+// ceil(T*S / slots) / S, plus a small charge per extra split for the partials
+// written and summed (about 4% of a tile time each, measured).
+inline int choose_tail_splits(int64_t tail, int64_t slots, int groups) {
+  int best = 1;
+  double best_cost = 1.0;
+  for (int s = 2; s <= kGemmMaxTailSplits && s <= groups; ++s) {
+    const double rounds = (double)((tail * s + slots - 1) / slots);
+    const double cost = rounds / s + 0.04 * (s - 1);
+    if (cost < best_cost - 1e-9) {
+      best_cost = cost;
+      best = s;
+    }
+  }
+  return best;
+}
+
+// `am`: the GEMM A mode of the launch (gemm::A_PLAIN or gemm::A_SILU_PACKED).
+inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am) {
   Plan pl;
   pl.n_cg = (int)(n / 256);
   const int groups = (int)(k / 128);
@@ -211,32 +231,48 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
     // + the zero entry + the bias corrections [group][16] fp32
     const size_t stage = pl.x_bytes + 16 + (size_t)max_groups * skinny::kMaxM * 4;
     pl.lds = std::max(stage, (size_t)m * skinny::kCols * 4);
+    pl.partial_bytes = pl.splits > 1 ? align_up((size_t)pl.splits * (size_t)m * (size_t)n * 4) : 0;
   } else {
     pl.skinny = false;
+    // 128-row tiles (two workgroups per CU) where M fills them; the SiLU-gated
+    // variant keeps 64-row tiles (its A staging registers leave no room).
 #ifdef LB_GEMM_MB
-    pl.mb = LB_GEMM_MB;
+    pl.mb = (LB_GEMM_MB == 8 && am != gemm::A_PLAIN) ? 4 : LB_GEMM_MB;
 #else
-    pl.mb = m > 32 ? 4 : 2;  // MB = 8 does not fit two workgroups per CU in registers
+    pl.mb = (m >= 128 && am == gemm::A_PLAIN) ? 8 : (m > 32 ? 4 : 2);
 #endif
     const int64_t bm = 16 * pl.mb;
     pl.n_mb = (int)((m + bm - 1) / bm);
     const int64_t tiles = (int64_t)pl.n_cg * pl.n_mb;
-    int s = 1;
-    if (tiles < kGemmTargetWGs) s = (int)((kGemmTargetWGs + tiles - 1) / tiles);
-    if (s > groups) s = groups;
-    if (s < 1) s = 1;
-    if (s > 1 && workspace_len < tiles + 1) s = 1;
-    pl.splits = s;
+    const int64_t slots = (int64_t)gemm::wgs_per_cu(pl.mb, am) * device_cus();
+    int64_t full = (tiles / slots) * slots;
+    int64_t tail = tiles - full;
+    int s = tail > 0 ? choose_tail_splits(tail, slots, groups) : 1;
+#ifdef LB_GEMM_TAIL_SPLITS
+    if (tail > 0) s = LB_GEMM_TAIL_SPLITS < groups ? LB_GEMM_TAIL_SPLITS : groups;
+#endif
+    if (s > 1 && workspace_len < 1 + tail) s = 1;
+    // partials are addressed through a 32-bit buffer resource
+    while (s > 1 && (size_t)tail * s * 16 * pl.mb * gemm::kThreads * 4 >= ((size_t)1 << 31)) --s;
+    if (s == 1) {
+      full = tiles;
+      tail = 0;
+    }
+    pl.full_tiles = (int)full;
+    pl.tail_tiles = (int)tail;
+    pl.tail_splits = s;
+    pl.wgs = full + tail * s;
+    pl.partial_bytes = tail > 0 ? align_up((size_t)tail * s * 16 * pl.mb * gemm::kThreads * 4) : 0;
   }
-  pl.partial_bytes = pl.splits > 1 ? align_up((size_t)pl.splits * (size_t)m * (size_t)n * 4) : 0;
   pl.keys_bytes = align_up((size_t)m * (size_t)pl.n_cg * 8);
   return pl;
 }
 
-// Workspace entries a launch uses: [0] the argmax arrival counter, [1 + tile]
-// the split-K counters of each output tile.
+// Workspace entries a launch uses: [0] the argmax arrival counter, [1 + t]
+// the split counters (decode: every column tile; GEMM: every tail tile).
 inline int64_t counters_needed(const Plan& pl, bool argmax) {
-  if (pl.splits > 1) return 1 + (int64_t)pl.n_cg * pl.n_mb;
+  if (pl.skinny && pl.splits > 1) return 1 + (int64_t)pl.n_cg;
+  if (!pl.skinny && pl.tail_tiles > 0) return 1 + (int64_t)pl.tail_tiles;
   return argmax ? 1 : 0;
 }
 
@@ -270,7 +306,7 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   // The GEMM kernel addresses A, B and s through 32-bit buffer resources.
   const int64_t a_bytes = m * k * 2 * (var == V_SILU ? 2 : 1);
   if (m > skinny::kMaxM && (a_bytes >= (1LL << 31) || k * n / 2 >= (1LL << 31))) return LB_ERR_PROB_SHAPE;
-  const Plan pl = make_plan(m, n, k, workspace_len);
+  const Plan pl = make_plan(m, n, k, workspace_len, var == V_SILU ? gemm::A_SILU_PACKED : gemm::A_PLAIN);
   if (workspace_len < counters_needed(pl, var == V_ARGMAX)) return LB_ERR_WORKSPACE;
   const size_t need = pl.partial_bytes + (var == V_ARGMAX ? pl.keys_bytes : 0);
   if (need > 0 && (!scratch || scratch_bytes < need)) return LB_ERR_SCRATCH;
@@ -302,9 +338,10 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   p.a = a; p.b = reinterpret_cast<const uint32_t*>(b); p.s = s; p.c = c;
   p.counters = workspace; p.partial = partial; p.tile_keys = keys;
   p.argmax_state = argmax_state; p.argmax_out = argmax_out;
-  p.m = (int)m; p.n = (int)n; p.k = (int)k; p.grouped = grouped; p.splits = pl.splits;
+  p.m = (int)m; p.n = (int)n; p.k = (int)k; p.grouped = grouped;
+  p.full_tiles = pl.full_tiles; p.tail_splits = pl.tail_splits; p.partial_bytes = (uint32_t)pl.partial_bytes;
   p.kp_total = (int)(k / 32); p.n_cg = pl.n_cg; p.n_mb = pl.n_mb;
-  dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, (unsigned)pl.n_mb);
+  dim3 grid((unsigned)pl.wgs, 1, 1);
 #define LB_GM(MBV, AMV, EPV, GV) \
   hipLaunchKernelGGL((gemm::marlin_gemm_kernel<MBV, AMV, EPV, GV>), grid, dim3(gemm::kThreads), 0, st, p)
 #define LB_GM_G(MBV, AMV, EPV)                      \
@@ -319,7 +356,10 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
     else LB_GM_G(2, AMV, EPV);                  \
   } while (0)
   if (var == V_PLAIN) LB_GM_MB(gemm::A_PLAIN, gemm::EPI_STORE);
-  else if (var == V_SILU) LB_GM_MB(gemm::A_SILU_PACKED, gemm::EPI_STORE);
+  else if (var == V_SILU) {  // 64-row tiles at most (see make_plan)
+    if (pl.mb == 4) LB_GM_G(4, gemm::A_SILU_PACKED, gemm::EPI_STORE);
+    else LB_GM_G(2, gemm::A_SILU_PACKED, gemm::EPI_STORE);
+  }
   else LB_GM_MB(gemm::A_PLAIN, gemm::EPI_ARGMAX);
 #undef LB_GM_MB
 #undef LB_GM_G
@@ -352,8 +392,10 @@ extern "C" size_t lb_marlin_scratch_bytes(int64_t prob_m, int64_t prob_n, int64_
   (void)groupsize;
   if (prob_m <= 0 || prob_n <= 0 || prob_k <= 0 || prob_n % 256 || prob_k % 128) return 0;
   // Plan with an unconstrained workspace: the largest scratch any plan uses.
-  const marlin::Plan pl = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX);
-  return pl.partial_bytes + pl.keys_bytes;
+  // Largest over the variants (the SiLU-gated one may use other tiles).
+  const marlin::Plan a = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN);
+  const marlin::Plan b = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_SILU_PACKED);
+  return std::max(a.partial_bytes + a.keys_bytes, b.partial_bytes + b.keys_bytes);
 }
 
 extern "C" int lb_marlin_gemm(const uint16_t* A, const int32_t* B, uint16_t* C, const uint16_t* s,

@@ -11,16 +11,20 @@
 //
 // Workgroup tile: (16*MB rows) x 256 columns; wave w owns 64-column chunk w.
 // The k loop runs in stages of one scale group (128 k = 4 MFMA steps):
-//   A  -- the stage's rows are read from global memory (16 B per item, one
-//         row's 256 bytes by 16 consecutive threads) one stage ahead into
-//         registers, then written to a double-buffered LDS tile in fragment
-//         order (entry (d, g, r) = A[r][32d + 16(g>>1) + 4(g&1) + {0..3}] ++
-//         the same + 8); one __syncthreads per stage.
-//   B  -- each lane's slots and the group scales two stages ahead.
-// The stage loop is unrolled by two so that buffer and slot indices are
-// compile-time constants.  Optional split-K over S workgroups uses the same
-// deterministic hand-off as the decode kernel (fp32 partials in scratch, the
-// last arrival sums them in split order).
+//   A  -- plain A goes from global memory straight into a double-buffered LDS
+//         tile by buffer-to-LDS DMA, one dword per lane, in fragment order;
+//         the SiLU-gated A is loaded into registers, gated, and written to LDS.
+//   B  -- each lane's four slots and the group's scales, in registers.
+// The loads of stage s + 1 are issued a share per MFMA step during stage s;
+// one s_waitcnt and one barrier end each stage.  The stage loop is unrolled by
+// two so that buffer and slot indices are compile-time constants.
+//
+// Schedule: the first `full_tiles` workgroups each compute one tile whole --
+// as many tiles as fill every resident slot a whole number of times -- and
+// the remaining tiles are split over K among `tail_splits` workgroups each, so
+// that the last partial round of tiles does not leave most CUs idle.  Split
+// workgroups publish fp32 partials to scratch; the last to arrive at the
+// tile's counter sums them in split order (deterministic) and finishes.
 
 #pragma once
 #include <type_traits>
@@ -41,18 +45,24 @@ struct Params {
   const uint32_t* b;
   const uint16_t* s;
   uint16_t* c;
-  int32_t* counters;     // [0] argmax arrival counter, [1 + tile] split-K counters
-  float* partial;        // [S][M][N]
+  int32_t* counters;     // [0] argmax arrival counter, [1 + t] counters of split tail tile t
+  float* partial;        // [tail tile][split][accumulator register][thread] fp32x4
+  uint32_t partial_bytes;
   uint64_t* tile_keys;   // [M][n_cg]
   int64_t* argmax_state;
   int64_t* argmax_out;
   int m, n, k;
   int grouped;
-  int splits;
+  int full_tiles;        // tiles computed whole, by workgroups 0 .. full_tiles - 1
+  int tail_splits;       // the remaining tiles are split over K among this many workgroups each
   int kp_total;
   int n_cg;
   int n_mb;
 };
+
+// Workgroups per CU each variant is compiled for (register-limited); the host
+// plans the tail split with the same figures.
+__host__ __device__ constexpr int wgs_per_cu(int mb, int am) { return mb >= 8 ? 2 : (am == A_SILU_PACKED ? 2 : 3); }
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
 
@@ -68,14 +78,6 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int lane, int off) 
   return ((uint64_t)hi << 32) | lo;
 }
 
-__device__ __forceinline__ void split_range(const Params& p, int split, int& kp0, int& kp1) {
-  const int groups = p.kp_total >> 2;
-  const int g0 = (int)(((int64_t)groups * split) / p.splits);
-  const int g1 = (int)(((int64_t)groups * (split + 1)) / p.splits);
-  kp0 = g0 << 2;
-  kp1 = g1 << 2;
-}
-
 // Raw buffer resource (gfx9 V#: stride 0, 32-bit data format).  Loads at or
 // past num_records return zero: rows of the last M block beyond M use that.
 __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, uint32_t bytes) {
@@ -84,30 +86,94 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, ui
 
 constexpr int kSteps = 4;  // 32-k steps per stage (one scale group of 128)
 
+// Buffer descriptor words for inline assembly: base, 16-bit base high with
+// stride 0, range in bytes, and the same format word as buffer_of.
+__device__ __forceinline__ u32x4 buffer_words(const void* base, uint32_t bytes) {
+  const uint64_t a = (uint64_t)(uintptr_t)base;
+  return (u32x4){(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
+}
+
+// s_waitcnt vmcnt(N) as the builtin, so that the compiler's own wait
+// placement knows which of its loads have completed (an assembly wait is
+// opaque to it and it would wait again, for newer loads too).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt is six bits");
+  __builtin_amdgcn_s_waitcnt(((N & 0x30) << 10) | (N & 0xf) | (0x7 << 4) | (0xf << 8));
+}
+
+// N consecutive rows of A straight into LDS, one dword per lane per row:
+// row n's instruction reads buffer offset voff + min(row0 + n*row_step,
+// row_max) + soff and lane L writes LDS byte address lds + n*lds_step + 4L.
+// The row offset goes in the scalar offset, which the descriptor's range
+// check does not cover, so it is clamped to the last row (rows past M are
+// read from row M - 1 and never stored).  Issued as assembly so that the
+// compiler does not treat the DMA as a pending write to every LDS location
+// (it would wait for all outstanding DMA before each LDS read) and keeps no
+// per-row addresses live; callers order it with an explicit s_waitcnt vmcnt
+// and a barrier before the data is read.
+template <int N, int LdsStep>
+__device__ __forceinline__ void dma_rows_lds(const u32x4& rsrc, uint32_t lds, uint32_t voff, uint32_t row0,
+                                             uint32_t row_step, uint32_t row_max, uint32_t soff) {
+  uint32_t row, t, m0_saved;
+  // M0 is reserved to the compiler: saved and restored around the DMA.
+  asm volatile(
+      "s_mov_b32 %[m0s], m0\n\t"
+      "s_mov_b32 m0, %[lds]\n\t"
+      "s_mov_b32 %[row], %[row0]\n\t"
+      ".rept %c[n]\n\t"
+      "s_min_u32 %[t], %[row], %[rmax]\n\t"
+      "s_add_u32 %[t], %[t], %[soff]\n\t"
+      "buffer_load_dword %[v], %[rsrc], %[t] offen lds\n\t"
+      "s_add_u32 m0, m0, %c[lstep]\n\t"
+      "s_add_u32 %[row], %[row], %[rstep]\n\t"
+      ".endr\n\t"
+      "s_mov_b32 m0, %[m0s]"
+      : [row] "=&s"(row), [t] "=&s"(t), [m0s] "=&s"(m0_saved)
+      : [lds] "s"(lds), [row0] "s"(row0), [rmax] "s"(row_max), [soff] "s"(soff), [rstep] "s"(row_step),
+        [v] "v"(voff), [rsrc] "s"(rsrc), [n] "i"(N), [lstep] "i"(LdsStep)
+      : "memory", "scc");
+}
+
 template <int MB, int AM, int EPI, bool GROUPED>
-__global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
+__global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kernel(Params p) {
   constexpr int BM = 16 * MB;
-  // A stage in LDS, fragment order, double-buffered: entry (d, g, r) is 16 B:
-  // A[r][32d + 16(g>>1) + 4(g&1) + {0..3}] ++ the same + 8.  Each (d, g) block
-  // is padded by one entry so that the staging writes of one row, which go to
-  // different (d, g) blocks, land in different banks.
+  // Plain A is staged by LDS DMA (buffer loads straight into LDS, no
+  // registers); the SiLU-gated A goes through registers to be computed.
+  constexpr bool kDma = AM == A_PLAIN;
+  // DMA layout: one 272-byte LDS row per A row (256 B of the stage + 16 B pad,
+  // so the 16 rows of a fragment read fall in distinct banks); within a row,
+  // 16-byte entry (d, g) at (4d + g) holds the fragment A[r][32d + 16(g>>1) +
+  // 4(g&1) + {0..3}] ++ the same + 8 -- the DMA of a row writes lane L's
+  // dword to entry L/4, dword L%4, so each lane fetches the dword that belongs
+  // there.  Register layout: entry (d, g, r) at ((4d + g) * kBlk + r), each
+  // (d, g) block padded by one entry so that the staging writes of one row,
+  // which go to different blocks, land in different banks.
+  constexpr int kRowU4 = 17;
   constexpr int kBlk = BM + 1;
-  __shared__ __attribute__((aligned(16))) uint4 afr[2][kSteps * 4 * kBlk];
+  constexpr int kBufU4 = kDma ? BM * kRowU4 : kSteps * 4 * kBlk;
+  __shared__ __attribute__((aligned(16))) uint4 afr[2][kBufU4];
   __shared__ int s_prev;
   __shared__ uint64_t s_keys[kWaves][BM];
 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int cg = blockIdx.x;
-  const int split = blockIdx.y;
-  const int mb = blockIdx.z;
+  // work unit: a whole tile, or split `split` of a tail tile
+  const int bid = blockIdx.x;
+  int tile = bid, split = 0, nsplit = 1;
+  if (bid >= p.full_tiles) {
+    nsplit = p.tail_splits;
+    const int u = bid - p.full_tiles;
+    tile = p.full_tiles + u / nsplit;
+    split = u - (u / nsplit) * nsplit;
+  }
+  const int mb = tile / p.n_cg;
+  const int cg = tile - mb * p.n_cg;
   const int m0 = mb * BM;
-
-  int kp0, kp1;
-  split_range(p, split, kp0, kp1);
-  const int st0 = kp0 / kSteps;         // first scale group (stage)
-  const int nst = (kp1 - kp0) / kSteps; // stages of this split
+  const int groups = p.kp_total >> 2;
+  const int st0 = (int)(((int64_t)groups * split) / nsplit);           // first scale group (stage)
+  const int nst = (int)(((int64_t)groups * (split + 1)) / nsplit) - st0;  // stages of this unit
 
   const int chunk = cg * kWaves + wave;
   const uint32_t row_bytes = 8u * (uint32_t)p.n;
@@ -132,9 +198,36 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
   static_assert(kAItems % kThreads == 0, "A staging items");
   const int64_t a_row_halves = AM == A_SILU_PACKED ? 2 * (int64_t)p.k : (int64_t)p.k;
   const __amdgpu_buffer_rsrc_t ra = buffer_of(p.a, (uint32_t)((int64_t)p.m * a_row_halves * 2));
-  uint4 areg[kAPer];
+  uint4 areg[kDma ? 1 : kAPer];
   uint4 ureg[AM == A_SILU_PACKED ? kAPer : 1];
-  auto load_a = [&](int stage) {
+  // DMA: lane L of a row's instruction fetches the dword of entry (d, g) =
+  // (L/4 / 4, L/4 % 4), dword e = L % 4: halves 32d + 16(g>>1) + 4(g&1) +
+  // 2(e&1) + 8(e>>1) and the next.
+  const uint32_t dma_k = (uint32_t)(32 * ((lane >> 2) >> 2) + 16 * (((lane >> 2) & 3) >> 1) + 4 * ((lane >> 2) & 1) +
+                                    2 * (lane & 1) + 8 * ((lane >> 1) & 1));
+  const u32x4 ra_words = buffer_words(p.a, (uint32_t)((int64_t)p.m * a_row_halves * 2));
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
+  const uint32_t afr_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(&afr[0][0]);
+  constexpr int kRowsPerWave = BM / kWaves;
+  // The row and stage offsets are wave-uniform and go in the scalar offset
+  // (one vector offset, the lane's dword, serves every row).  The scalar
+  // offset is outside the descriptor's range check, so rows past M are
+  // clamped to row M - 1 (read, never stored) to keep every access in bounds.
+  const uint32_t dma_v = dma_k * 2u;
+  const uint32_t a_row_bytes = (uint32_t)p.k * 2u;
+  const uint32_t a_row_max = (uint32_t)(p.m - 1) * a_row_bytes;
+  // rows [t0, t0 + N) of this wave's share of stage `stage` into LDS buffer `buf`
+  auto dma_rows = [&](int stage, int buf, int t0, auto n) __attribute__((always_inline)) {
+    const int r = wave_u * kRowsPerWave + t0;
+    dma_rows_lds<decltype(n)::value, kRowU4 * 16>(ra_words, afr_lds + (uint32_t)((buf * kBufU4 + r * kRowU4) * 16),
+                                                  dma_v, (uint32_t)(m0 + r) * a_row_bytes, a_row_bytes, a_row_max,
+                                                  (uint32_t)stage * 256u);
+  };
+  auto dma_a = [&](int stage, int buf) __attribute__((always_inline)) {
+    dma_rows(stage, buf, 0, std::integral_constant<int, kRowsPerWave>{});
+  };
+  auto load_a = [&](int stage) __attribute__((always_inline)) {
+    if (kDma) return;
 #pragma unroll
     for (int t = 0; t < kAPer; ++t) {
       const int item = tid + t * kThreads;
@@ -145,7 +238,8 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
         ureg[t] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, off + 2u * (uint32_t)p.k, 0, 0));
     }
   };
-  auto store_a = [&](int buf) {
+  auto store_a = [&](int buf) __attribute__((always_inline)) {
+    if (kDma) return;
 #pragma unroll
     for (int t = 0; t < kAPer; ++t) {
       const int item = tid + t * kThreads;
@@ -176,7 +270,7 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
   // ---- B ring: two stages of (4 slots + the group's scales) per lane ----
   u32x4 bst[2][kSteps];
   u32x4 sst[2];
-  auto load_b = [&](int slot, int stage) {
+  auto load_b = [&](int slot, int stage) __attribute__((always_inline)) {
 #pragma unroll
     for (int d = 0; d < kSteps; ++d)
       bst[slot][d] = __builtin_bit_cast(
@@ -192,7 +286,23 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[j][i] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  auto compute = [&](int buf, int slot) {
+  // dequantise step d of B slot `slot` into four fp16 fragments: exact fp16
+  // (q - 8) times the fp16 group scale, the rounding of the reference's __hmul2
+  auto dequant = [&](int slot, int d, const f16x2 (&sc)[4], f16x8 (&bf)[4]) __attribute__((always_inline)) {
+    const u32x4 own = bst[slot][d];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t partner = (uint32_t)__builtin_amdgcn_mov_dpp((int)own[j], 0x128, 0xf, 0xf, false);  // row_ror:8
+      const uint32_t v0 = __builtin_amdgcn_perm(own[j], partner, psel);
+      const uint32_t v1 = v0 >> 8;
+      const f16x2 b0 = nib_lo_to_h2(v0, nk) * sc[j];
+      const f16x2 b1 = nib_lo_to_h2(v1, nk) * sc[j];
+      const f16x2 b2 = nib_hi_to_h2(v0, nk) * sc[j];
+      const f16x2 b3 = nib_hi_to_h2(v1, nk) * sc[j];
+      bf[j] = __builtin_bit_cast(f16x8, make_uint4(as_u32(b0), as_u32(b1), as_u32(b2), as_u32(b3)));
+    }
+  };
+  auto compute = [&](int buf, int slot, auto hook) __attribute__((always_inline)) {
     f16x2 sc[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -202,31 +312,60 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
 #pragma unroll
     for (int d = 0; d < kSteps; ++d) {
       f16x8 bfrag[4];
-      const u32x4 own = bst[slot][d];
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const uint32_t partner = (uint32_t)__builtin_amdgcn_mov_dpp((int)own[j], 0x128, 0xf, 0xf, false);  // row_ror:8
-        const uint32_t v0 = __builtin_amdgcn_perm(own[j], partner, psel);
-        const uint32_t v1 = v0 >> 8;
-        // exact fp16 (q - 8) times the fp16 group scale: the rounding of the reference's __hmul2
-        const f16x2 b0 = nib_lo_to_h2(v0, nk) * sc[j];
-        const f16x2 b1 = nib_lo_to_h2(v1, nk) * sc[j];
-        const f16x2 b2 = nib_hi_to_h2(v0, nk) * sc[j];
-        const f16x2 b3 = nib_hi_to_h2(v1, nk) * sc[j];
-        bfrag[j] = __builtin_bit_cast(f16x8, make_uint4(as_u32(b0), as_u32(b1), as_u32(b2), as_u32(b3)));
-      }
-      const uint4* abase = &afr[buf][(d * 4 + g) * kBlk + (lane & 15)];
+      dequant(slot, d, sc, bfrag);
+      hook(d);
+      const uint4* abase = kDma ? &afr[buf][(lane & 15) * kRowU4 + d * 4 + g] : &afr[buf][(d * 4 + g) * kBlk + (lane & 15)];
 #pragma unroll
       for (int i = 0; i < MB; ++i) {
-        const f16x8 afrag = __builtin_bit_cast(f16x8, abase[16 * i]);
+        const f16x8 afrag = __builtin_bit_cast(f16x8, abase[16 * i * (kDma ? kRowU4 : 1)]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag[j], acc[j][i], 0, 0, 0);
       }
+      __builtin_amdgcn_sched_barrier(0);  // bound the registers live across steps
     }
   };
 
-  // ---- pipeline: A one stage ahead (registers -> LDS), B two stages ahead ----
-  if (nst > 0) {
+  auto no_hook = [](int) __attribute__((always_inline)) {};
+
+  // ---- pipeline (DMA A): the loads of stage s + 1 are issued a share per
+  // step during stage s -- A into the LDS buffer stage s - 1 used, each B slot
+  // into the registers of the slot just dequantised -- and land before the
+  // barrier that ends stage s ----
+  if (kDma && nst > 0) {
+    dma_a(st0, 0);
+    load_b(0, st0);
+    wait_vmcnt<0>();
+    __syncthreads();
+    auto stage = [&](int s, auto par) __attribute__((always_inline)) {
+      constexpr int c = decltype(par)::value;
+      const bool more = s + 1 < nst;
+      const int nx = st0 + s + 1;
+      auto hook = [&](int d) __attribute__((always_inline)) {
+        if (!more) return;
+        static_assert(kRowsPerWave % kSteps == 0, "rows per step");
+        constexpr int kPer = kRowsPerWave / kSteps;
+        dma_rows(nx, c ^ 1, d * kPer, std::integral_constant<int, kPer>{});
+        // step d's B slot is reloaded with stage s + 1's right after its
+        // dequant, so one set of B registers serves both stages
+        bst[0][d] = __builtin_bit_cast(
+            u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, b_off, (uint32_t)(nx * 8 + 2 * d) * row_bytes, 0));
+        if (GROUPED && d == 0)
+          sst[0] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, s_off, (uint32_t)nx * (uint32_t)p.n * 2u, 0));
+      };
+      compute(c, 0, hook);
+      wait_vmcnt<0>();
+      __syncthreads();
+    };
+    int s = 0;
+    for (; s + 1 < nst; s += 2) {
+      stage(s, std::integral_constant<int, 0>{});
+      stage(s + 1, std::integral_constant<int, 1>{});
+    }
+    if (s < nst) stage(s, std::integral_constant<int, 0>{});
+  }
+  // ---- pipeline (register A): A one stage ahead, B two stages ahead ----
+  if (!kDma && nst > 0) {
     load_a(st0);
     load_b(0, st0);
     if (nst > 1) load_b(1, st0 + 1);
@@ -235,19 +374,22 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
     if (nst > 1) load_a(st0 + 1);
     // Stage s uses LDS buffer and B slot s & 1; unrolled by two so that both
     // are compile-time constants (no indexed register access).
-    auto stage = [&](int s, auto par) {
+    auto stage = [&](int s, auto par) __attribute__((always_inline)) {
       constexpr int c = decltype(par)::value;
-      compute(c, c);
+      compute(c, c, no_hook);
       if (s + 2 < nst) load_b(c, st0 + s + 2);
       if (s + 1 < nst) store_a(c ^ 1);  // buffer c ^ 1 was last read in stage s - 1
       __syncthreads();
       if (s + 2 < nst) load_a(st0 + s + 2);
     };
-    for (int s = 0; s < nst; s += 2) {
+    // pairs of stages, then an odd last one: no exit from the middle of the
+    // loop body, so the compiler's wait placement sees one state per edge
+    int s = 0;
+    for (; s + 1 < nst; s += 2) {
       stage(s, std::integral_constant<int, 0>{});
-      if (s + 1 >= nst) break;
       stage(s + 1, std::integral_constant<int, 1>{});
     }
+    if (s < nst) stage(s, std::integral_constant<int, 0>{});
   }
 
   // ---- epilogue ----
@@ -255,37 +397,47 @@ __global__ __launch_bounds__(kThreads) void marlin_gemm_kernel(Params p) {
   const int rbase = m0 + 4 * (lane >> 4);
   const int ccol = chunk * 64 + (lane & 15);
 
-  if (p.splits > 1) {
-    float* part = p.partial + (int64_t)split * p.m * p.n;
+  if (nsplit > 1) {
+    // partials of tail tile t: [split][accumulator register q][thread], 16
+    // bytes each, so that one register of the workgroup is 4 KB contiguous
+    constexpr int kQ = 4 * MB;
+    constexpr uint32_t kRegBytes = kThreads * 16u;
+    const int t = tile - p.full_tiles;
+    const __amdgpu_buffer_rsrc_t rp = buffer_of(p.partial, p.partial_bytes);
+    const uint32_t tile_off = (uint32_t)(t * nsplit) * kQ * kRegBytes + (uint32_t)tid * 16u;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < MB; ++i)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = rbase + 16 * i + e;
-          if (r < p.m) publish(part + (int64_t)r * p.n + ccol + 16 * j, acc[j][i][e]);
-        }
+        publish16(rp, tile_off + (uint32_t)(split * kQ + j * MB + i) * kRegBytes, acc[j][i]);
     wait_published();
     __syncthreads();
-    int32_t* ctr = p.counters + 1 + cg + mb * p.n_cg;
+    int32_t* ctr = p.counters + 1 + t;
     if (tid == 0) s_prev = arrive(ctr);
     __syncthreads();
-    if (s_prev != p.splits - 1) return;
+    if (s_prev != nsplit - 1) return;
+    // The last arrival sums the splits in split order (its own from
+    // registers), one column block of MB registers per batch of loads.
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 4; ++j) {
+      f32x4 sum[MB];
 #pragma unroll
-      for (int i = 0; i < MB; ++i)
+      for (int i = 0; i < MB; ++i) sum[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+      for (int sp = 0; sp < nsplit; ++sp) {
+        if (sp == split) {
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int r = rbase + 16 * i + e;
-          float sum = 0.f;
-          if (r < p.m) {
-            for (int sp = 0; sp < p.splits; ++sp)
-              sum += collect(p.partial + ((int64_t)sp * p.m + r) * p.n + ccol + 16 * j);
-          }
-          acc[j][i][e] = sum;
+          for (int i = 0; i < MB; ++i) sum[i] += acc[j][i];
+        } else {
+          f32x4 v[MB];
+#pragma unroll
+          for (int i = 0; i < MB; ++i) v[i] = collect16(rp, tile_off + (uint32_t)(sp * kQ + j * MB + i) * kRegBytes);
+#pragma unroll
+          for (int i = 0; i < MB; ++i) sum[i] += v[i];
         }
+      }
+#pragma unroll
+      for (int i = 0; i < MB; ++i) acc[j][i] = sum[i];
+    }
     if (tid == 0) reset_counter(ctr);
   }
 

@@ -174,7 +174,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   float* corr = reinterpret_cast<float*>(afr + n_frag + 1);
   const int64_t a_row_stride = AM == A_SILU_PACKED ? 2 * (int64_t)p.k : (int64_t)p.k;
   uint4 gv[kStageUnroll], uv[kStageUnroll];
-  auto stage_load = [&](int base) {
+  auto stage_load = [&](int base) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
       const int it = min(base + u * kThreads + tid, items - 1);
@@ -184,7 +184,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
       if (AM == A_SILU_PACKED) uv[u] = *reinterpret_cast<const uint4*>(src + p.k);
     }
   };
-  auto stage_store = [&](int base) {
+  auto stage_store = [&](int base) __attribute__((always_inline)) {
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
       const int it = base + u * kThreads + tid;
