@@ -191,13 +191,13 @@ inline int device_cus() {
 // GEMM tail split: the tiles left after the last full round of resident
 // workgroups are split over K.  S minimises the tail's length in tile times,
 // ceil(T*S / slots) / S, plus a small charge per extra split for the partials
-// written and summed (about 4% of a tile time each, measured).
+// written and summed (about 6% of a tile time each, measured).
 inline int choose_tail_splits(int64_t tail, int64_t slots, int groups) {
   int best = 1;
   double best_cost = 1.0;
   for (int s = 2; s <= kGemmMaxTailSplits && s <= groups; ++s) {
     const double rounds = (double)((tail * s + slots - 1) / slots);
-    const double cost = rounds / s + 0.04 * (s - 1);
+    const double cost = rounds / s + 0.06 * (s - 1);
     if (cost < best_cost - 1e-9) {
       best_cost = cost;
       best = s;

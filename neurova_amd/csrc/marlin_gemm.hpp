@@ -86,12 +86,6 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, ui
 
 constexpr int kSteps = 4;  // 32-k steps per stage (one scale group of 128)
 
-// Buffer descriptor words for inline assembly: base, 16-bit base high with
-// stride 0, range in bytes, and the same format word as buffer_of.
-__device__ __forceinline__ u32x4 buffer_words(const void* base, uint32_t bytes) {
-  const uint64_t a = (uint64_t)(uintptr_t)base;
-  return (u32x4){(uint32_t)a, (uint32_t)(a >> 32) & 0xffffu, bytes, 0x00020000u};
-}
 
 // s_waitcnt vmcnt(N) as the builtin, so that the compiler's own wait
 // placement knows which of its loads have completed (an assembly wait is
@@ -102,38 +96,10 @@ __device__ __forceinline__ void wait_vmcnt() {
   __builtin_amdgcn_s_waitcnt(((N & 0x30) << 10) | (N & 0xf) | (0x7 << 4) | (0xf << 8));
 }
 
-// N consecutive rows of A straight into LDS, one dword per lane per row:
-// row n's instruction reads buffer offset voff + min(row0 + n*row_step,
-// row_max) + soff and lane L writes LDS byte address lds + n*lds_step + 4L.
-// The row offset goes in the scalar offset, which the descriptor's range
-// check does not cover, so it is clamped to the last row (rows past M are
-// read from row M - 1 and never stored).  Issued as assembly so that the
-// compiler does not treat the DMA as a pending write to every LDS location
-// (it would wait for all outstanding DMA before each LDS read) and keeps no
-// per-row addresses live; callers order it with an explicit s_waitcnt vmcnt
-// and a barrier before the data is read.
-template <int N, int LdsStep>
-__device__ __forceinline__ void dma_rows_lds(const u32x4& rsrc, uint32_t lds, uint32_t voff, uint32_t row0,
-                                             uint32_t row_step, uint32_t row_max, uint32_t soff) {
-  uint32_t row, t, m0_saved;
-  // M0 is reserved to the compiler: saved and restored around the DMA.
-  asm volatile(
-      "s_mov_b32 %[m0s], m0\n\t"
-      "s_mov_b32 m0, %[lds]\n\t"
-      "s_mov_b32 %[row], %[row0]\n\t"
-      ".rept %c[n]\n\t"
-      "s_min_u32 %[t], %[row], %[rmax]\n\t"
-      "s_add_u32 %[t], %[t], %[soff]\n\t"
-      "buffer_load_dword %[v], %[rsrc], %[t] offen lds\n\t"
-      "s_add_u32 m0, m0, %c[lstep]\n\t"
-      "s_add_u32 %[row], %[row], %[rstep]\n\t"
-      ".endr\n\t"
-      "s_mov_b32 m0, %[m0s]"
-      : [row] "=&s"(row), [t] "=&s"(t), [m0s] "=&s"(m0_saved)
-      : [lds] "s"(lds), [row0] "s"(row0), [rmax] "s"(row_max), [soff] "s"(soff), [rstep] "s"(row_step),
-        [v] "v"(voff), [rsrc] "s"(rsrc), [n] "i"(N), [lstep] "i"(LdsStep)
-      : "memory", "scc");
-}
+
+#ifndef LB_GEMM_INTERLEAVE
+#define LB_GEMM_INTERLEAVE 1
+#endif
 
 template <int MB, int AM, int EPI, bool GROUPED>
 __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kernel(Params p) {
@@ -152,7 +118,12 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   constexpr int kRowU4 = 17;
   constexpr int kBlk = BM + 1;
   constexpr int kBufU4 = kDma ? BM * kRowU4 : kSteps * 4 * kBlk;
-  __shared__ __attribute__((aligned(16))) uint4 afr[2][kBufU4];
+  // two separate arrays (not one [2][...]): the compiler's wait placement then
+  // tells the buffer-to-LDS DMA into one buffer from reads of the other, and
+  // waits for a DMA only before reads of the buffer it writes
+  __shared__ __attribute__((aligned(16))) uint4 afr0[kBufU4];
+  __shared__ __attribute__((aligned(16))) uint4 afr1[kBufU4];
+  auto afr = [&](int buf) __attribute__((always_inline)) -> uint4* { return buf ? afr1 : afr0; };
   __shared__ int s_prev;
   __shared__ uint64_t s_keys[kWaves][BM];
 
@@ -205,9 +176,7 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   // 2(e&1) + 8(e>>1) and the next.
   const uint32_t dma_k = (uint32_t)(32 * ((lane >> 2) >> 2) + 16 * (((lane >> 2) & 3) >> 1) + 4 * ((lane >> 2) & 1) +
                                     2 * (lane & 1) + 8 * ((lane >> 1) & 1));
-  const u32x4 ra_words = buffer_words(p.a, (uint32_t)((int64_t)p.m * a_row_halves * 2));
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
-  const uint32_t afr_lds = (uint32_t)(uintptr_t)(__attribute__((address_space(3))) void*)(&afr[0][0]);
   constexpr int kRowsPerWave = BM / kWaves;
   // The row and stage offsets are wave-uniform and go in the scalar offset
   // (one vector offset, the lane's dword, serves every row).  The scalar
@@ -216,12 +185,27 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   const uint32_t dma_v = dma_k * 2u;
   const uint32_t a_row_bytes = (uint32_t)p.k * 2u;
   const uint32_t a_row_max = (uint32_t)(p.m - 1) * a_row_bytes;
-  // rows [t0, t0 + N) of this wave's share of stage `stage` into LDS buffer `buf`
+  // rows [t0, t0 + N) of this wave's share of stage `stage` into LDS buffer
+  // `buf`: one dword per lane per row, lane L writing row byte 4L.  The row
+  // and stage offsets are wave-uniform and go in the scalar offset, which the
+  // descriptor's range check does not cover, so rows past M are clamped to
+  // row M - 1 (read, never stored).  The first row's offset passes through
+  // an empty asm so that the compiler recomputes the row offsets per stage
+  // with a few scalar adds instead of keeping every row's offset live.
   auto dma_rows = [&](int stage, int buf, int t0, auto n) __attribute__((always_inline)) {
-    const int r = wave_u * kRowsPerWave + t0;
-    dma_rows_lds<decltype(n)::value, kRowU4 * 16>(ra_words, afr_lds + (uint32_t)((buf * kBufU4 + r * kRowU4) * 16),
-                                                  dma_v, (uint32_t)(m0 + r) * a_row_bytes, a_row_bytes, a_row_max,
-                                                  (uint32_t)stage * 256u);
+    const int r0 = wave_u * kRowsPerWave + t0;
+    uint32_t row = (uint32_t)(m0 + r0) * a_row_bytes;
+    uint32_t lds_off = (uint32_t)(r0 * kRowU4 * 16);
+    asm volatile("" : "+s"(row), "+s"(lds_off));
+    const uint32_t stage_off = (uint32_t)stage * 256u;
+    char* dst = reinterpret_cast<char*>(afr(buf)) + lds_off;
+#pragma unroll
+    for (int t = 0; t < decltype(n)::value; ++t) {
+      const uint32_t soff = (row < a_row_max ? row : a_row_max) + stage_off;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(
+          ra, (__attribute__((address_space(3))) void*)(dst + t * kRowU4 * 16), 4, dma_v, soff, 0, 0);
+      row += a_row_bytes;
+    }
   };
   auto dma_a = [&](int stage, int buf) __attribute__((always_inline)) {
     dma_rows(stage, buf, 0, std::integral_constant<int, kRowsPerWave>{});
@@ -260,8 +244,8 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
       }
       // octet o = 4d + 2prow + half: halves 0..3 -> (d, g = 2prow), 4..7 -> (d, g = 2prow + 1)
       const int d = o >> 2, pr = (o >> 1) & 1, half = o & 1;
-      uint2* dst0 = reinterpret_cast<uint2*>(&afr[buf][(d * 4 + 2 * pr) * kBlk + r]) + half;
-      uint2* dst1 = reinterpret_cast<uint2*>(&afr[buf][(d * 4 + 2 * pr + 1) * kBlk + r]) + half;
+      uint2* dst0 = reinterpret_cast<uint2*>(&afr(buf)[(d * 4 + 2 * pr) * kBlk + r]) + half;
+      uint2* dst1 = reinterpret_cast<uint2*>(&afr(buf)[(d * 4 + 2 * pr + 1) * kBlk + r]) + half;
       *dst0 = make_uint2(w.x, w.y);
       *dst1 = make_uint2(w.z, w.w);
     }
@@ -314,7 +298,7 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
       f16x8 bfrag[4];
       dequant(slot, d, sc, bfrag);
       hook(d);
-      const uint4* abase = kDma ? &afr[buf][(lane & 15) * kRowU4 + d * 4 + g] : &afr[buf][(d * 4 + g) * kBlk + (lane & 15)];
+      const uint4* abase = kDma ? &afr(buf)[(lane & 15) * kRowU4 + d * 4 + g] : &afr(buf)[(d * 4 + g) * kBlk + (lane & 15)];
 #pragma unroll
       for (int i = 0; i < MB; ++i) {
         const f16x8 afrag = __builtin_bit_cast(f16x8, abase[16 * i * (kDma ? kRowU4 : 1)]);
@@ -327,34 +311,157 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
 
   auto no_hook = [](int) __attribute__((always_inline)) {};
 
-  // ---- pipeline (DMA A): the loads of stage s + 1 are issued a share per
-  // step during stage s -- A into the LDS buffer stage s - 1 used, each B slot
-  // into the registers of the slot just dequantised -- and land before the
-  // barrier that ends stage s ----
+  // ---- interleaved dequant (plain A) ----
+  // One step's dequant split into 8 phases of one or two VALU instructions
+  // per B word, so that step d + 1's dequant can be spread over the MFMAs of
+  // step d (VALU instructions between a wave's MFMAs run in their shadow):
+  //   0: DPP partner, byte perm    1: >> 8, low nibbles of v0
+  //   2: high of v0, low of v1     3: high of v1, bias of (lo v0)
+  //   4: bias of (lo v1), (hi v0)  5: bias of (hi v1), scale (lo v0)
+  //   6: scale (lo v1), (hi v0)    7: scale (hi v1)
+  struct DqTmp {
+    uint32_t v0[4], v1[4], lo0[4], hi0[4], lo1[4], hi1[4];
+    f16x2 b[4][4];
+  };
+  auto dq_word = [&](DqTmp& q, int d, const f16x2 (&sc)[4], int ph, int j) __attribute__((always_inline)) {
+    const f16x2 k1032 = {(f16)1032.0f, (f16)1032.0f};
+    const f16x2 k16 = {(f16)0.0625f, (f16)0.0625f}, k72 = {(f16)-72.0f, (f16)-72.0f};
+    switch (ph) {
+      case 0: {
+        const uint32_t own = bst[0][d][j];
+        const uint32_t partner = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0x128, 0xf, 0xf, false);  // row_ror:8
+        q.v0[j] = __builtin_amdgcn_perm(own, partner, psel);
+        break;
+      }
+      case 1:
+        q.v1[j] = q.v0[j] >> 8;
+        q.lo0[j] = and_or(q.v0[j], nk.lo_mask, nk.magic);
+        break;
+      case 2:
+        q.hi0[j] = and_or(q.v0[j], nk.hi_mask, nk.magic);
+        q.lo1[j] = and_or(q.v1[j], nk.lo_mask, nk.magic);
+        break;
+      case 3:
+        q.hi1[j] = and_or(q.v1[j], nk.hi_mask, nk.magic);
+        q.b[j][0] = as_h2(q.lo0[j]) - k1032;
+        break;
+      case 4:
+        q.b[j][1] = as_h2(q.lo1[j]) - k1032;
+        q.b[j][2] = as_h2(q.hi0[j]) * k16 + k72;
+        break;
+      case 5:
+        q.b[j][3] = as_h2(q.hi1[j]) * k16 + k72;
+        q.b[j][0] = q.b[j][0] * sc[j];
+        break;
+      case 6:
+        q.b[j][1] = q.b[j][1] * sc[j];
+        q.b[j][2] = q.b[j][2] * sc[j];
+        break;
+      default:
+        q.b[j][3] = q.b[j][3] * sc[j];
+        break;
+    }
+  };
+  auto dq_pack = [&](const DqTmp& q, f16x8 (&bf)[4]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j)
+      bf[j] = __builtin_bit_cast(f16x8, make_uint4(as_u32(q.b[j][0]), as_u32(q.b[j][1]), as_u32(q.b[j][2]),
+                                                   as_u32(q.b[j][3])));
+  };
+  // One stage of plain-A compute: step 0's dequant up front, then step d's
+  // MFMAs (row block i's A fragment read two blocks ahead) each followed by
+  // a share of step d + 1's dequant; `hook(d)` runs once step d's B slot has
+  // been dequantised.
+  auto compute_interleaved = [&](int buf, auto hook) __attribute__((always_inline)) {
+    f16x2 sc[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const uint32_t h = GROUPED ? ((sst[0][j] >> (16 * hsel)) & 0xffffu) : 0x3c00u;  // fp16 1.0
+      sc[j] = as_h2(h | (h << 16));
+    }
+    f16x8 bcur[4];
+    {
+      DqTmp q;
+#pragma unroll
+      for (int ph = 0; ph < 8; ++ph)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) dq_word(q, 0, sc, ph, j);
+      dq_pack(q, bcur);
+    }
+    hook(0);
+    __builtin_amdgcn_sched_barrier(0);
+    constexpr int kPhPerRow = 8 / MB > 0 ? 8 / MB : 1;
+#pragma unroll
+    for (int d = 0; d < kSteps; ++d) {
+      const uint4* abase = &afr(buf)[(lane & 15) * kRowU4 + d * 4 + g];
+      DqTmp q;
+      f16x8 ar[MB];
+      ar[0] = __builtin_bit_cast(f16x8, abase[0]);
+      if (MB > 1) ar[1] = __builtin_bit_cast(f16x8, abase[16 * kRowU4]);
+#pragma unroll
+      for (int i = 0; i < MB; ++i) {
+        if (i + 2 < MB) ar[i + 2] = __builtin_bit_cast(f16x8, abase[16 * (i + 2) * kRowU4]);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ar[i], bcur[j], acc[j][i], 0, 0, 0);
+          if (d + 1 < kSteps) {
+#pragma unroll
+            for (int t = 0; t < kPhPerRow; ++t) {
+              const int ph = i * kPhPerRow + t;
+              if (ph < 8) dq_word(q, d + 1, sc, ph, j);
+            }
+          }
+          __builtin_amdgcn_sched_barrier(0);
+        }
+      }
+      if (d + 1 < kSteps) {
+        // phases not covered by the row blocks (MB > 8 never happens; MB < 8 covers all)
+        dq_pack(q, bcur);
+        hook(d + 1);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  };
+
+  // ---- pipeline (DMA A): the loads of stage s + 1 are issued during stage
+  // s -- A into the LDS buffer stage s - 1 used, each B slot into the
+  // registers of the slot just dequantised.  A, the scales and B slots 0 and
+  // 1 land before the barrier that ends stage s; slots 2 and 3 are waited for
+  // where stage s + 1 dequantises them ----
   if (kDma && nst > 0) {
     dma_a(st0, 0);
     load_b(0, st0);
     wait_vmcnt<0>();
     __syncthreads();
+    // Every stage issues the next stage's loads -- the last one re-reads its
+    // own stage into the buffer and registers nobody reads afterwards -- so
+    // that the loop body has no load-skipping branches and the compiler's
+    // wait placement stays exact.
     auto stage = [&](int s, auto par) __attribute__((always_inline)) {
       constexpr int c = decltype(par)::value;
-      const bool more = s + 1 < nst;
-      const int nx = st0 + s + 1;
+      const int nx = st0 + (s + 1 < nst ? s + 1 : s);
+      // issue order: scale, B slot 0, A rows 0 .. R/2 (after step 0's
+      // dequant); B slot 1, A rows R/2 .. R (after step 1's); B slots 2, 3
       auto hook = [&](int d) __attribute__((always_inline)) {
-        if (!more) return;
-        static_assert(kRowsPerWave % kSteps == 0, "rows per step");
-        constexpr int kPer = kRowsPerWave / kSteps;
-        dma_rows(nx, c ^ 1, d * kPer, std::integral_constant<int, kPer>{});
+        if (GROUPED && d == 0)
+          sst[0] = __builtin_bit_cast(
+              u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, s_off, (uint32_t)nx * (uint32_t)p.n * 2u, 0));
         // step d's B slot is reloaded with stage s + 1's right after its
         // dequant, so one set of B registers serves both stages
         bst[0][d] = __builtin_bit_cast(
             u32x4, __builtin_amdgcn_raw_buffer_load_b128(rb, b_off, (uint32_t)(nx * 8 + 2 * d) * row_bytes, 0));
-        if (GROUPED && d == 0)
-          sst[0] = __builtin_bit_cast(
-              u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, s_off, (uint32_t)nx * (uint32_t)p.n * 2u, 0));
+        static_assert(kRowsPerWave % 2 == 0, "rows per half");
+        if (d < 2) dma_rows(nx, c ^ 1, d * (kRowsPerWave / 2), std::integral_constant<int, kRowsPerWave / 2>{});
       };
+#if LB_GEMM_INTERLEAVE
+      compute_interleaved(c, hook);
+#else
       compute(c, 0, hook);
-      wait_vmcnt<0>();
+#endif
+      // everything but B slots 2 and 3 of stage s + 1 has landed: this
+      // wave's A rows of buffer c ^ 1 among them; the barrier makes every
+      // wave's rows visible and retires buffer c
+      wait_vmcnt<2>();
       __syncthreads();
     };
     int s = 0;
@@ -363,6 +470,8 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
       stage(s + 1, std::integral_constant<int, 1>{});
     }
     if (s < nst) stage(s, std::integral_constant<int, 0>{});
+    // the last stage's extra DMA must land before the workgroup's LDS is released
+    wait_vmcnt<0>();
   }
   // ---- pipeline (register A): A one stage ahead, B two stages ahead ----
   if (!kDma && nst > 0) {
