@@ -124,6 +124,15 @@ __device__ __forceinline__ f32x4 collect16(__amdgpu_buffer_rsrc_t r, uint32_t of
   return __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, kSc1));
 }
 
+// Workgroup barrier for LDS data only: waits for this wave's LDS operations,
+// not for its outstanding global loads (__syncthreads' fence would also wait
+// for every in-flight vector-memory load, e.g. a prefetch ring).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
+}
+
 // Waits until every vector-memory operation this thread issued (loads,
 // stores, atomics) has been acknowledged; the memory clobber keeps the
 // compiler from moving memory accesses across it.

@@ -206,7 +206,7 @@ inline int choose_tail_splits(int64_t tail, int64_t slots, int groups) {
   return best;
 }
 
-// `am`: the GEMM A mode of the launch (gemm::A_PLAIN or gemm::A_SILU_PACKED).
+// `am`: the A mode of the launch (gemm::A_PLAIN or gemm::A_SILU_PACKED).
 inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am) {
   Plan pl;
   pl.n_cg = (int)(n / 256);

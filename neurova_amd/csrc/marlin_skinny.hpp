@@ -243,7 +243,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
     stage_store(base);
   }
   if (tid == 0) afr[n_frag] = (u32x4){0, 0, 0, 0};
-  __syncthreads();
+  lds_barrier();  // LDS only: the weight ring stays in flight
 
   // Bias correction.  The MFMA sees 1024 + q against x (k = 0..7 of a row) and
   // 1024 + 16q against x/16 (k = 8..15), i.e. x*q + 1024x and x~*q + 64x~ with
@@ -261,7 +261,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
     }
     corr[t] = -(1032.f * lo + 1152.f * hi);
   }
-  __syncthreads();
+  lds_barrier();  // LDS only: the weight ring stays in flight
 
   // A fragment address: rows >= M read the zero entry.
   const bool a_live = mrow < mrows;

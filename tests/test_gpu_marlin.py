@@ -115,6 +115,52 @@ def test_wide_decode_vs_oracle(dev, m, k, group):
         assert_exact_scale(got, ref, O.marlin_gemm_exact(x, qw, sp, group), what=f"wide m={m} k={k}")
 
 
+@pytest.mark.parametrize("m,k,n,group", [
+    (1, 5120, 17408, 128),
+    (2, 5120, 17408, -1),
+    (1, 5120, 16640, 128),
+    (3, 1024, 16640, 128),
+    (1, 2048, 16640, -1),
+    (8, 1024, 17408, 128),
+])
+def test_wide_decode_leftovers_vs_oracle(dev, m, k, n, group):
+    """Decode at N just above 64 columns per CU (16384): 256-column tiles that
+    do not divide evenly over the CUs, up to M = 8, both scale modes, and
+    repeated launches bit-identical."""
+    print_case("wide-left", m, k, n, group)
+    codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=900 + m + k + n)
+    got = _run_gemm(dev, x, qw, sp, group)
+    ref = O.marlin_gemm(x, qw, sp, group)
+    exact = assert_close_f16(got, ref, what=f"wide-left m={m} k={k} n={n} g={group}")
+    if group <= 0:
+        assert exact > 0.9
+        _assert_per_column_rounding(got, codes, x, sp)
+    else:
+        assert_exact_scale(got, ref, O.marlin_gemm_exact(x, qw, sp, group), what=f"wide-left m={m} k={k} n={n}")
+    # repeated launches are bit-identical (split partials are summed in split order)
+    again = _run_gemm(dev, x, qw, sp, group)
+    assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
+
+
+@pytest.mark.parametrize("m", [1, 3])
+def test_wide_silu_packed_vs_oracle(dev, m):
+    import torch
+    from neurova_amd import capi
+
+    k, n = 2048, 17408
+    print_case("wide-silu", m, k, n)
+    _, qw, _, sp, _ = O.make_marlin_inputs(m, k, n, 128, seed=70 + m)
+    mixed = np.random.default_rng(70 + m).normal(0, 1, (m, 2 * k)).astype(np.float16)
+    c = torch.empty((m, n), dtype=torch.float16, device=dev)
+    ws = _ws(dev, n)
+    st = capi.marlin_gemm_silu_packed(to_dev(mixed, dev), to_dev(qw, dev), c, to_dev(sp, dev), ws, 128,
+                                      _scratch(dev, m, n, k, 128))
+    assert st == 0
+    torch.cuda.synchronize()
+    assert int(ws.abs().sum()) == 0
+    assert_close_f16(to_np(c), O.marlin_gemm_silu_packed(mixed, qw, sp, k, 128), what=f"wide-silu m={m}")
+
+
 @pytest.mark.parametrize("m", [17, 33, 64, 100, 256, 300])
 def test_gemm_vs_oracle(dev, m):
     k, n = 1024, 768
