@@ -97,25 +97,23 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 
-#ifndef LB_GEMM_INTERLEAVE
-#define LB_GEMM_INTERLEAVE 1
-#endif
-
 template <int MB, int AM, int EPI, bool GROUPED>
 __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kernel(Params p) {
   constexpr int BM = 16 * MB;
   // Plain A is staged by LDS DMA (buffer loads straight into LDS, no
   // registers); the SiLU-gated A goes through registers to be computed.
   constexpr bool kDma = AM == A_PLAIN;
-  // DMA layout: one 272-byte LDS row per A row (256 B of the stage + 16 B pad,
-  // so the 16 rows of a fragment read fall in distinct banks); within a row,
-  // 16-byte entry (d, g) at (4d + g) holds the fragment A[r][32d + 16(g>>1) +
-  // 4(g&1) + {0..3}] ++ the same + 8 -- the DMA of a row writes lane L's
-  // dword to entry L/4, dword L%4, so each lane fetches the dword that belongs
-  // there.  Register layout: entry (d, g, r) at ((4d + g) * kBlk + r), each
-  // (d, g) block padded by one entry so that the staging writes of one row,
-  // which go to different blocks, land in different banks.
-  constexpr int kRowU4 = 17;
+  // DMA layout: one 256-byte LDS row per A row, the stage's 128 k in natural
+  // order as 16 chunks of 8 halves, chunk c stored at position c ^ (r & 7)
+  // (so that the 16 rows of a fragment read fall in different banks).  A
+  // 16-byte-per-lane DMA writes four rows (1 KB) per instruction: lane L
+  // writes position L & 15 of row L >> 4 and fetches the chunk that belongs
+  // there.  A fragment -- A[r][32d + 16(g>>1) + 4(g&1) + {0..3}] ++ the same
+  // + 8 -- is the (g&1) half of chunks 4d + 2(g>>1) and 4d + 2(g>>1) + 1: two
+  // 8-byte reads.  Register layout: entry (d, g, r) at ((4d + g) * kBlk + r),
+  // each (d, g) block padded by one entry so that the staging writes of one
+  // row, which go to different blocks, land in different banks.
+  constexpr int kRowU4 = 16;
   constexpr int kBlk = BM + 1;
   constexpr int kBufU4 = kDma ? BM * kRowU4 : kSteps * 4 * kBlk;
   // two separate arrays (not one [2][...]): the compiler's wait placement then
@@ -171,40 +169,35 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   const __amdgpu_buffer_rsrc_t ra = buffer_of(p.a, (uint32_t)((int64_t)p.m * a_row_halves * 2));
   uint4 areg[kDma ? 1 : kAPer];
   uint4 ureg[AM == A_SILU_PACKED ? kAPer : 1];
-  // DMA: lane L of a row's instruction fetches the dword of entry (d, g) =
-  // (L/4 / 4, L/4 % 4), dword e = L % 4: halves 32d + 16(g>>1) + 4(g&1) +
-  // 2(e&1) + 8(e>>1) and the next.
-  const uint32_t dma_k = (uint32_t)(32 * ((lane >> 2) >> 2) + 16 * (((lane >> 2) & 3) >> 1) + 4 * ((lane >> 2) & 1) +
-                                    2 * (lane & 1) + 8 * ((lane >> 1) & 1));
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   constexpr int kRowsPerWave = BM / kWaves;
-  // The row and stage offsets are wave-uniform and go in the scalar offset
-  // (one vector offset, the lane's dword, serves every row).  The scalar
-  // offset is outside the descriptor's range check, so rows past M are
-  // clamped to row M - 1 (read, never stored) to keep every access in bounds.
-  const uint32_t dma_v = dma_k * 2u;
+  // DMA source of lane L in a four-row instruction: row 4j + (L >> 4) of the
+  // wave's share, chunk (L & 15) ^ (row & 7); (row & 7) = 4(j & 1) + (L >> 4)
+  // since the share starts at a multiple of 8.  The whole row offset is in
+  // the vector offset, which the descriptor's range check covers: rows at or
+  // past M read zeros and are never stored.  The stage offset (< 2K bytes)
+  // is the scalar offset.
+  static_assert(kRowsPerWave % 8 == 0, "DMA row blocks");
   const uint32_t a_row_bytes = (uint32_t)p.k * 2u;
-  const uint32_t a_row_max = (uint32_t)(p.m - 1) * a_row_bytes;
-  // rows [t0, t0 + N) of this wave's share of stage `stage` into LDS buffer
-  // `buf`: one dword per lane per row, lane L writing row byte 4L.  The row
-  // and stage offsets are wave-uniform and go in the scalar offset, which the
-  // descriptor's range check does not cover, so rows past M are clamped to
-  // row M - 1 (read, never stored).  The first row's offset passes through
-  // an empty asm so that the compiler recomputes the row offsets per stage
-  // with a few scalar adds instead of keeping every row's offset live.
+  const int lrow = lane >> 4;
+  const uint32_t dma_row0 = (uint32_t)(m0 + wave_u * kRowsPerWave + lrow) * a_row_bytes;
+  // rows [t0, t0 + N) of this wave's share of stage `stage` into LDS buffer `buf`
   auto dma_rows = [&](int stage, int buf, int t0, auto n) __attribute__((always_inline)) {
-    const int r0 = wave_u * kRowsPerWave + t0;
-    uint32_t row = (uint32_t)(m0 + r0) * a_row_bytes;
-    uint32_t lds_off = (uint32_t)(r0 * kRowU4 * 16);
-    asm volatile("" : "+s"(row), "+s"(lds_off));
-    const uint32_t stage_off = (uint32_t)stage * 256u;
-    char* dst = reinterpret_cast<char*>(afr(buf)) + lds_off;
+    static_assert(decltype(n)::value % 4 == 0, "four rows per DMA");
+    char* dst = reinterpret_cast<char*>(afr(buf)) + (wave_u * kRowsPerWave + t0) * 256;
+    // opaque per call, so that the per-instruction offsets are recomputed
+    // (one scalar multiply and one vector add) instead of all kept live
+    uint32_t rows4 = 4u * a_row_bytes;
+    asm volatile("" : "+s"(rows4));
+    // lane offsets of even / odd row blocks, recomputed per call (not kept live)
+    const uint32_t v_even = dma_row0 + (uint32_t)((lane & 15) ^ lrow) * 16u;
+    const uint32_t v_odd = dma_row0 + (uint32_t)((lane & 15) ^ (4 + lrow)) * 16u;
 #pragma unroll
-    for (int t = 0; t < decltype(n)::value; ++t) {
-      const uint32_t soff = (row < a_row_max ? row : a_row_max) + stage_off;
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(
-          ra, (__attribute__((address_space(3))) void*)(dst + t * kRowU4 * 16), 4, dma_v, soff, 0, 0);
-      row += a_row_bytes;
+    for (int jj = 0; jj < decltype(n)::value / 4; ++jj) {  // constant trip count: fully unrolled
+      const int j = t0 / 4 + jj;
+      const uint32_t voff = ((j & 1) ? v_odd : v_even) + (uint32_t)j * rows4;
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(dst + jj * 4 * 256), 16,
+                                               voff, (uint32_t)stage * 256u, 0, 0);
     }
   };
   auto dma_a = [&](int stage, int buf) __attribute__((always_inline)) {
@@ -298,10 +291,10 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
       f16x8 bfrag[4];
       dequant(slot, d, sc, bfrag);
       hook(d);
-      const uint4* abase = kDma ? &afr(buf)[(lane & 15) * kRowU4 + d * 4 + g] : &afr(buf)[(d * 4 + g) * kBlk + (lane & 15)];
+      const uint4* abase = &afr(buf)[(d * 4 + g) * kBlk + (lane & 15)];
 #pragma unroll
       for (int i = 0; i < MB; ++i) {
-        const f16x8 afrag = __builtin_bit_cast(f16x8, abase[16 * i * (kDma ? kRowU4 : 1)]);
+        const f16x8 afrag = __builtin_bit_cast(f16x8, abase[16 * i]);
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag[j], acc[j][i], 0, 0, 0);
       }
@@ -314,7 +307,8 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   // ---- interleaved dequant (plain A) ----
   // One step's dequant split into 8 phases of one or two VALU instructions
   // per B word, so that step d + 1's dequant can be spread over the MFMAs of
-  // step d (VALU instructions between a wave's MFMAs run in their shadow):
+  // step d (VALU instructions between a wave's MFMAs run in their shadow),
+  // one word after another:
   //   0: DPP partner, byte perm    1: >> 8, low nibbles of v0
   //   2: high of v0, low of v1     3: high of v1, bias of (lo v0)
   //   4: bias of (lo v1), (hi v0)  5: bias of (hi v1), scale (lo v0)
@@ -368,6 +362,18 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
       bf[j] = __builtin_bit_cast(f16x8, make_uint4(as_u32(q.b[j][0]), as_u32(q.b[j][1]), as_u32(q.b[j][2]),
                                                    as_u32(q.b[j][3])));
   };
+  // A fragment (d, g) of row 16i + r, r = lane & 15: the (g&1) halves of
+  // chunks c = 4d + 2(g>>1) and c + 1, stored at c ^ (r & 7).  With s = r & 7,
+  // (4d + 2h) ^ s = 4(d ^ s2) + ((2h ^ s) & 3) (s2 = bit 2 of s), so the byte
+  // offset is a per-lane base for d even / odd plus 128 (d >> 1) + 4096 i.
+  // (the chunk + 1 entry is the position ^ 1, i.e. the byte offset ^ 16)
+  uint32_t a_off_lo[2];
+  {
+    const int sw = lane & 7, s2 = sw >> 2, h2 = 2 * (g >> 1);
+#pragma unroll
+    for (int e = 0; e < 2; ++e)
+      a_off_lo[e] = (uint32_t)((lane & 15) * 256 + 8 * (g & 1) + 64 * (e ^ s2) + 16 * ((h2 ^ sw) & 3));
+  }
   // One stage of plain-A compute: step 0's dequant up front, then step d's
   // MFMAs (row block i's A fragment read two blocks ahead) each followed by
   // a share of step d + 1's dequant; `hook(d)` runs once step d's B slot has
@@ -390,37 +396,53 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
     }
     hook(0);
     __builtin_amdgcn_sched_barrier(0);
-    constexpr int kPhPerRow = 8 / MB > 0 ? 8 / MB : 1;
-#pragma unroll
-    for (int d = 0; d < kSteps; ++d) {
-      const uint4* abase = &afr(buf)[(lane & 15) * kRowU4 + d * 4 + g];
+    // 32 (word, phase) pairs per step, spread over the 4*MB MFMA slots word
+    // by word (a word's phases are dependent, one slot apart at least; one
+    // word's temporaries live at a time)
+    constexpr int kPhPerSlot = 8 / MB > 0 ? 8 / MB : 1;
+    // steps as compile-time constants (a plain loop over d is not always
+    // unrolled, and a runtime d would index the B registers dynamically)
+    auto step = [&](auto dc) __attribute__((always_inline)) {
+      constexpr int d = decltype(dc)::value;
+      const char* abuf = reinterpret_cast<const char*>(afr(buf));
+      const uint32_t off_lo = a_off_lo[d & 1], off_hi = off_lo ^ 16u;
+      auto read_a = [&](int i) __attribute__((always_inline)) {
+        const int o = (d >> 1) * 128 + i * 16 * 256;
+        const uint2 lo = *reinterpret_cast<const uint2*>(abuf + off_lo + o);
+        const uint2 hi = *reinterpret_cast<const uint2*>(abuf + off_hi + o);
+        return __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
+      };
       DqTmp q;
       f16x8 ar[MB];
-      ar[0] = __builtin_bit_cast(f16x8, abase[0]);
-      if (MB > 1) ar[1] = __builtin_bit_cast(f16x8, abase[16 * kRowU4]);
+      ar[0] = read_a(0);
+      if (MB > 1) ar[1] = read_a(1);
 #pragma unroll
       for (int i = 0; i < MB; ++i) {
-        if (i + 2 < MB) ar[i + 2] = __builtin_bit_cast(f16x8, abase[16 * (i + 2) * kRowU4]);
+        if (i + 2 < MB) ar[i + 2] = read_a(i + 2);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ar[i], bcur[j], acc[j][i], 0, 0, 0);
           if (d + 1 < kSteps) {
 #pragma unroll
-            for (int t = 0; t < kPhPerRow; ++t) {
-              const int ph = i * kPhPerRow + t;
-              if (ph < 8) dq_word(q, d + 1, sc, ph, j);
+            for (int t = 0; t < kPhPerSlot; ++t) {
+              const int pw = (i * 4 + j) * kPhPerSlot + t;
+              if (pw < 32) dq_word(q, d + 1, sc, pw & 7, pw >> 3);
             }
           }
           __builtin_amdgcn_sched_barrier(0);
         }
       }
       if (d + 1 < kSteps) {
-        // phases not covered by the row blocks (MB > 8 never happens; MB < 8 covers all)
         dq_pack(q, bcur);
         hook(d + 1);
       }
       __builtin_amdgcn_sched_barrier(0);
-    }
+    };
+    static_assert(kSteps == 4, "four MFMA steps per stage");
+    step(std::integral_constant<int, 0>{});
+    step(std::integral_constant<int, 1>{});
+    step(std::integral_constant<int, 2>{});
+    step(std::integral_constant<int, 3>{});
   };
 
   // ---- pipeline (DMA A): the loads of stage s + 1 are issued during stage
@@ -453,11 +475,7 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
         static_assert(kRowsPerWave % 2 == 0, "rows per half");
         if (d < 2) dma_rows(nx, c ^ 1, d * (kRowsPerWave / 2), std::integral_constant<int, kRowsPerWave / 2>{});
       };
-#if LB_GEMM_INTERLEAVE
       compute_interleaved(c, hook);
-#else
-      compute(c, 0, hook);
-#endif
       // everything but B slots 2 and 3 of stage s + 1 has landed: this
       // wave's A rows of buffer c ^ 1 among them; the barrier makes every
       // wave's rows visible and retires buffer c
