@@ -97,6 +97,13 @@ __device__ __forceinline__ void wait_vmcnt() {
 }
 
 
+// An empty volatile asm that reads and rewrites a register value: the value
+// is computed before this point and not moved past it.
+template <class T>
+__device__ __forceinline__ void pin_vgpr(T& x) {
+  asm volatile("" : "+v"(x));
+}
+
 template <int MB, int AM, int EPI, bool GROUPED>
 __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kernel(Params p) {
   constexpr int BM = 16 * MB;
@@ -317,6 +324,9 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
     uint32_t v0[4], v1[4], lo0[4], hi0[4], lo1[4], hi1[4];
     f16x2 b[4][4];
   };
+  // Each phase's results pass through an empty volatile asm: that pins them
+  // to their slot (left alone, the compiler sinks the f16 arithmetic to the
+  // end of the step, where it runs exposed after the last MFMA).
   auto dq_word = [&](DqTmp& q, int d, const f16x2 (&sc)[4], int ph, int j) __attribute__((always_inline)) {
     const f16x2 k1032 = {(f16)1032.0f, (f16)1032.0f};
     const f16x2 k16 = {(f16)0.0625f, (f16)0.0625f}, k72 = {(f16)-72.0f, (f16)-72.0f};
@@ -325,34 +335,48 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
         const uint32_t own = bst[0][d][j];
         const uint32_t partner = (uint32_t)__builtin_amdgcn_mov_dpp((int)own, 0x128, 0xf, 0xf, false);  // row_ror:8
         q.v0[j] = __builtin_amdgcn_perm(own, partner, psel);
+        pin_vgpr(q.v0[j]);
         break;
       }
       case 1:
         q.v1[j] = q.v0[j] >> 8;
         q.lo0[j] = and_or(q.v0[j], nk.lo_mask, nk.magic);
+        pin_vgpr(q.v1[j]);
+        pin_vgpr(q.lo0[j]);
         break;
       case 2:
         q.hi0[j] = and_or(q.v0[j], nk.hi_mask, nk.magic);
         q.lo1[j] = and_or(q.v1[j], nk.lo_mask, nk.magic);
+        pin_vgpr(q.hi0[j]);
+        pin_vgpr(q.lo1[j]);
         break;
       case 3:
         q.hi1[j] = and_or(q.v1[j], nk.hi_mask, nk.magic);
         q.b[j][0] = as_h2(q.lo0[j]) - k1032;
+        pin_vgpr(q.hi1[j]);
+        pin_vgpr(q.b[j][0]);
         break;
       case 4:
         q.b[j][1] = as_h2(q.lo1[j]) - k1032;
         q.b[j][2] = as_h2(q.hi0[j]) * k16 + k72;
+        pin_vgpr(q.b[j][1]);
+        pin_vgpr(q.b[j][2]);
         break;
       case 5:
         q.b[j][3] = as_h2(q.hi1[j]) * k16 + k72;
         q.b[j][0] = q.b[j][0] * sc[j];
+        pin_vgpr(q.b[j][3]);
+        pin_vgpr(q.b[j][0]);
         break;
       case 6:
         q.b[j][1] = q.b[j][1] * sc[j];
         q.b[j][2] = q.b[j][2] * sc[j];
+        pin_vgpr(q.b[j][1]);
+        pin_vgpr(q.b[j][2]);
         break;
       default:
         q.b[j][3] = q.b[j][3] * sc[j];
+        pin_vgpr(q.b[j][3]);
         break;
     }
   };
@@ -410,6 +434,9 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
         const int o = (d >> 1) * 128 + i * 16 * 256;
         const uint2 lo = *reinterpret_cast<const uint2*>(abuf + off_lo + o);
         const uint2 hi = *reinterpret_cast<const uint2*>(abuf + off_hi + o);
+        // keeps one block's reads from merging with the next block's into a
+        // two-address read (whose halves land interleaved: register moves)
+        asm volatile("" ::: "memory");
         return __builtin_bit_cast(f16x8, make_uint4(lo.x, lo.y, hi.x, hi.y));
       };
       DqTmp q;
