@@ -111,8 +111,9 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   // registers); the SiLU-gated A goes through registers to be computed.
   constexpr bool kDma = AM == A_PLAIN;
   // DMA layout: one 256-byte LDS row per A row, the stage's 128 k in natural
-  // order as 16 chunks of 8 halves, chunk c stored at position c ^ (r & 7)
-  // (so that the 16 rows of a fragment read fall in different banks).  A
+  // order as 16 chunks of 8 halves, chunk c stored at position c ^ (r & 15)
+  // (so that the 16 rows of a fragment read fall in 16 different positions:
+  // no bank conflicts).  A
   // 16-byte-per-lane DMA writes four rows (1 KB) per instruction: lane L
   // writes position L & 15 of row L >> 4 and fetches the chunk that belongs
   // there.  A fragment -- A[r][32d + 16(g>>1) + 4(g&1) + {0..3}] ++ the same
@@ -178,13 +179,12 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   uint4 ureg[AM == A_SILU_PACKED ? kAPer : 1];
   const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   constexpr int kRowsPerWave = BM / kWaves;
-  // DMA source of lane L in a four-row instruction: row 4j + (L >> 4) of the
-  // wave's share, chunk (L & 15) ^ (row & 7); (row & 7) = 4(j & 1) + (L >> 4)
-  // since the share starts at a multiple of 8.  The whole row offset is in
-  // the vector offset, which the descriptor's range check covers: rows at or
-  // past M read zeros and are never stored.  The stage offset (< 2K bytes)
-  // is the scalar offset.
-  static_assert(kRowsPerWave % 8 == 0, "DMA row blocks");
+  // DMA source of lane L in a four-row instruction: tile row b + (L >> 4), b
+  // a multiple of 4, chunk (L & 15) ^ (row & 15) = ((L & 15) ^ (L >> 4)) ^
+  // (b & 12).  The whole row offset is in the vector offset, which the
+  // descriptor's range check covers: rows at or past M read zeros and are
+  // never stored.  The stage offset (< 2K bytes) is the scalar offset.
+  static_assert(kRowsPerWave % 4 == 0, "DMA row blocks");
   const uint32_t a_row_bytes = (uint32_t)p.k * 2u;
   const int lrow = lane >> 4;
   const uint32_t dma_row0 = (uint32_t)(m0 + wave_u * kRowsPerWave + lrow) * a_row_bytes;
@@ -196,13 +196,13 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
     // (one scalar multiply and one vector add) instead of all kept live
     uint32_t rows4 = 4u * a_row_bytes;
     asm volatile("" : "+s"(rows4));
-    // lane offsets of even / odd row blocks, recomputed per call (not kept live)
-    const uint32_t v_even = dma_row0 + (uint32_t)((lane & 15) ^ lrow) * 16u;
-    const uint32_t v_odd = dma_row0 + (uint32_t)((lane & 15) ^ (4 + lrow)) * 16u;
+    // the lane's chunk within a block starting at row b = 0 (mod 16), recomputed per call
+    const uint32_t x16 = (uint32_t)((lane & 15) ^ lrow) * 16u;
 #pragma unroll
     for (int jj = 0; jj < decltype(n)::value / 4; ++jj) {  // constant trip count: fully unrolled
       const int j = t0 / 4 + jj;
-      const uint32_t voff = ((j & 1) ? v_odd : v_even) + (uint32_t)j * rows4;
+      const uint32_t b12 = (uint32_t)((wave_u * kRowsPerWave + 4 * j) & 12) << 4;
+      const uint32_t voff = dma_row0 + (x16 ^ b12) + (uint32_t)j * rows4;
       __builtin_amdgcn_raw_ptr_buffer_load_lds(ra, (__attribute__((address_space(3))) void*)(dst + jj * 4 * 256), 16,
                                                voff, (uint32_t)stage * 256u, 0, 0);
     }
@@ -387,39 +387,40 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
                                                    as_u32(q.b[j][3])));
   };
   // A fragment (d, g) of row 16i + r, r = lane & 15: the (g&1) halves of
-  // chunks c = 4d + 2(g>>1) and c + 1, stored at c ^ (r & 7).  With s = r & 7,
-  // (4d + 2h) ^ s = 4(d ^ s2) + ((2h ^ s) & 3) (s2 = bit 2 of s), so the byte
-  // offset is a per-lane base for d even / odd plus 128 (d >> 1) + 4096 i.
-  // (the chunk + 1 entry is the position ^ 1, i.e. the byte offset ^ 16)
-  uint32_t a_off_lo[2];
-  {
-    const int sw = lane & 7, s2 = sw >> 2, h2 = 2 * (g >> 1);
-#pragma unroll
-    for (int e = 0; e < 2; ++e)
-      a_off_lo[e] = (uint32_t)((lane & 15) * 256 + 8 * (g & 1) + 64 * (e ^ s2) + 16 * ((h2 ^ sw) & 3));
-  }
-  // One stage of plain-A compute: step 0's dequant up front, then step d's
-  // MFMAs (row block i's A fragment read two blocks ahead) each followed by
-  // a share of step d + 1's dequant; `hook(d)` runs once step d's B slot has
-  // been dequantised.
-  auto compute_interleaved = [&](int buf, auto hook) __attribute__((always_inline)) {
-    f16x2 sc[4];
+  // chunks c = 4d + 2(g>>1) and c + 1, stored at positions c ^ r and
+  // (c ^ r) ^ 1 (c is even).  c ^ r = 4(d ^ (r >> 2)) + ((2(g>>1) ^ r) & 3),
+  // so step d's byte offset is a per-lane base XOR 64d (bits 6-7, which the
+  // rest of the base leaves clear), plus 4096 i; the chunk + 1 half is at the
+  // offset XOR 16.
+  const uint32_t a_off0 = (uint32_t)((lane & 15) * 256 + 8 * (g & 1) + 64 * ((lane & 15) >> 2) +
+                                     16 * ((2 * (g >> 1) ^ lane) & 3));
+  // The group scales of the stage whose B slots are in registers, as f16x2.
+  auto scales_of = [&](f16x2 (&sc)[4]) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
       const uint32_t h = GROUPED ? ((sst[0][j] >> (16 * hsel)) & 0xffffu) : 0x3c00u;  // fp16 1.0
       sc[j] = as_h2(h | (h << 16));
     }
-    f16x8 bcur[4];
-    {
-      DqTmp q;
+  };
+  // Step 0 of the first stage, dequantised up front (every later stage's step
+  // 0 is dequantised during the previous stage's last step).
+  auto dequant_first = [&](const f16x2 (&sc)[4], f16x8 (&bcur)[4]) __attribute__((always_inline)) {
+    DqTmp q;
 #pragma unroll
-      for (int ph = 0; ph < 8; ++ph)
+    for (int ph = 0; ph < 8; ++ph)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) dq_word(q, 0, sc, ph, j);
-      dq_pack(q, bcur);
-    }
-    hook(0);
-    __builtin_amdgcn_sched_barrier(0);
+      for (int j = 0; j < 4; ++j) dq_word(q, 0, sc, ph, j);
+    dq_pack(q, bcur);
+  };
+  // One stage of plain-A compute.  On entry `bcur` holds step 0's B
+  // fragments and `sc` the stage's scales.  Step d's MFMAs (row block i's A
+  // fragment read two blocks ahead) each carry a share of the dequant of step
+  // d + 1 -- for the last step, of the next stage's step 0, whose slot and
+  // scales were loaded by hook(0) -- so that no dequant runs outside the
+  // MFMAs' shadow.  `hook(d)` issues loads once step d's slot has been
+  // dequantised: hook(0) at the top of the stage, after its first A reads.
+  auto compute_interleaved = [&](int buf, auto hook, f16x2 (&sc)[4], f16x8 (&bcur)[4])
+      __attribute__((always_inline)) {
     // 32 (word, phase) pairs per step, spread over the 4*MB MFMA slots word
     // by word (a word's phases are dependent, one slot apart at least; one
     // word's temporaries live at a time)
@@ -428,10 +429,14 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
     // unrolled, and a runtime d would index the B registers dynamically)
     auto step = [&](auto dc) __attribute__((always_inline)) {
       constexpr int d = decltype(dc)::value;
+      constexpr int dn = (d + 1) % kSteps;  // slot dequantised during this step
       const char* abuf = reinterpret_cast<const char*>(afr(buf));
-      const uint32_t off_lo = a_off_lo[d & 1], off_hi = off_lo ^ 16u;
+      // recomputed per step (two XORs) rather than eight offsets kept live
+      uint32_t off_base = a_off0;
+      pin_vgpr(off_base);
+      const uint32_t off_lo = off_base ^ (uint32_t)(64 * d), off_hi = off_lo ^ 16u;
       auto read_a = [&](int i) __attribute__((always_inline)) {
-        const int o = (d >> 1) * 128 + i * 16 * 256;
+        const int o = i * 16 * 256;
         const uint2 lo = *reinterpret_cast<const uint2*>(abuf + off_lo + o);
         const uint2 hi = *reinterpret_cast<const uint2*>(abuf + off_hi + o);
         // keeps one block's reads from merging with the next block's into a
@@ -443,26 +448,25 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
       f16x8 ar[MB];
       ar[0] = read_a(0);
       if (MB > 1) ar[1] = read_a(1);
+      if (d == 0) hook(0);
+      if (d == kSteps - 1) scales_of(sc);  // the next stage's
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int i = 0; i < MB; ++i) {
         if (i + 2 < MB) ar[i + 2] = read_a(i + 2);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_f16(ar[i], bcur[j], acc[j][i], 0, 0, 0);
-          if (d + 1 < kSteps) {
 #pragma unroll
-            for (int t = 0; t < kPhPerSlot; ++t) {
-              const int pw = (i * 4 + j) * kPhPerSlot + t;
-              if (pw < 32) dq_word(q, d + 1, sc, pw & 7, pw >> 3);
-            }
+          for (int t = 0; t < kPhPerSlot; ++t) {
+            const int pw = (i * 4 + j) * kPhPerSlot + t;
+            if (pw < 32) dq_word(q, dn, sc, pw & 7, pw >> 3);
           }
           __builtin_amdgcn_sched_barrier(0);
         }
       }
-      if (d + 1 < kSteps) {
-        dq_pack(q, bcur);
-        hook(d + 1);
-      }
+      dq_pack(q, bcur);
+      if (d + 1 < kSteps) hook(d + 1);
       __builtin_amdgcn_sched_barrier(0);
     };
     static_assert(kSteps == 4, "four MFMA steps per stage");
@@ -482,6 +486,10 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
     load_b(0, st0);
     wait_vmcnt<0>();
     __syncthreads();
+    f16x2 sc[4];
+    f16x8 bcur[4];
+    scales_of(sc);
+    dequant_first(sc, bcur);
     // Every stage issues the next stage's loads -- the last one re-reads its
     // own stage into the buffer and registers nobody reads afterwards -- so
     // that the loop body has no load-skipping branches and the compiler's
@@ -489,8 +497,10 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
     auto stage = [&](int s, auto par) __attribute__((always_inline)) {
       constexpr int c = decltype(par)::value;
       const int nx = st0 + (s + 1 < nst ? s + 1 : s);
-      // issue order: scale, B slot 0, A rows 0 .. R/2 (after step 0's
-      // dequant); B slot 1, A rows R/2 .. R (after step 1's); B slots 2, 3
+      // issue order: scale, B slot 0, A rows 0 .. R/2 (top of the stage);
+      // B slot 1, A rows R/2 .. R (after step 1's dequant); B slots 2, 3.
+      // Slot 0 and the scales are dequantised in step 3, slots 1 .. 3 in
+      // steps 0 .. 2 of the next stage.
       auto hook = [&](int d) __attribute__((always_inline)) {
         if (GROUPED && d == 0)
           sst[0] = __builtin_bit_cast(
@@ -502,7 +512,7 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
         static_assert(kRowsPerWave % 2 == 0, "rows per half");
         if (d < 2) dma_rows(nx, c ^ 1, d * (kRowsPerWave / 2), std::integral_constant<int, kRowsPerWave / 2>{});
       };
-      compute_interleaved(c, hook);
+      compute_interleaved(c, hook, sc, bcur);
       // everything but B slots 2 and 3 of stage s + 1 has landed: this
       // wave's A rows of buffer c ^ 1 among them; the barrier makes every
       // wave's rows visible and retires buffer c
