@@ -94,7 +94,8 @@ def time_calls(torch, fn, n_sets, steps, warmup, use_graph=True):
         stream.wait_stream(side)
         torch.cuda.synchronize()
         graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(graph):
+        # capture on the warmed-up stream: its per-stream buffers already exist
+        with torch.cuda.graph(graph, stream=side):
             for i in range(n_sets):
                 fn(i)
         run_round = graph.replay

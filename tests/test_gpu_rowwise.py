@@ -65,6 +65,42 @@ def test_gemv_vs_oracle(dev, bits, rows, cols, group):
     assert_close_f16(got, O.rowwise_gemv(packed, scales, x[0], cols, group, bits), what=f"b{bits} {rows}x{cols} g{group}")
 
 
+def _pad_rows(packed, mult):
+    """Row stride padded to a multiple of `mult` bytes with junk (packed_cols >= need is allowed)."""
+    pad = (-packed.shape[1]) % mult
+    junk = np.full((packed.shape[0], pad), 0xA5, dtype=np.uint8)
+    return np.ascontiguousarray(np.concatenate([packed, junk], axis=1))
+
+
+@pytest.mark.parametrize("bits", [2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("rows,cols,group", [(37, 513, 128), (1, 259, 32), (6, 8192 + 96, 64), (301, 17408 + 7, 128)])
+def test_gemv_padded_stride_vs_oracle(dev, bits, rows, cols, group):
+    """Dword-multiple row strides take the batch-1 multi-row kernel: a partial last
+    32-code unit, an odd row count (last wave half empty), junk past each row's codes."""
+    print_case("gemv-padded", bits, rows, cols, group)
+    _, packed, scales, x = O.make_rowwise_inputs(rows, cols, bits, group, seed=bits * 11 + rows)
+    padded = _pad_rows(packed, 4)
+    got = _gemv(dev, padded, scales, x[0], cols, group, bits)
+    assert_close_f16(got, O.rowwise_gemv(packed, scales, x[0], cols, group, bits), what=f"b{bits} {rows}x{cols} g{group}")
+
+
+@pytest.mark.parametrize("bits", [2, 5, 8])
+def test_pair_padded_equals_two_singles(dev, bits):
+    import torch
+    import langburst_cuda as lc
+
+    cols = 1000
+    _, pa, sa, x = O.make_rowwise_inputs(33, cols, bits, 64, seed=170 + bits)
+    _, pb, sb, _ = O.make_rowwise_inputs(33, cols, bits, 64, seed=180 + bits)
+    qa, qb, sca, scb, xd = (to_dev(a, dev) for a in (_pad_rows(pa, 4), _pad_rows(pb, 4), sa, sb, x[0]))
+    ya = lc.lowbit_gemv(qa, sca, xd, cols, 64, bits)
+    yb = lc.lowbit_gemv(qb, scb, xd, cols, 64, bits)
+    pa_out, pb_out = lc.lowbit_gemv_pair(qa, sca, qb, scb, xd, cols, 64, bits)
+    torch.cuda.synchronize()
+    assert torch.equal(pa_out, ya) and torch.equal(pb_out, yb)
+    assert_close_f16(to_np(pb_out), O.rowwise_gemv(pb, sb, x[0], cols, 64, bits))
+
+
 @pytest.mark.parametrize("bits", [3, 4])
 def test_pair_equals_two_singles(dev, bits):
     import torch
