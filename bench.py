@@ -116,6 +116,81 @@ def time_calls(torch, fn, n_sets, steps, warmup, use_graph=True):
     return start.elapsed_time(stop), rounds * n_sets
 
 
+class DecodeStep:
+    """the projections of a 64-layer 27B-class decode step.
+
+    Per layer: QKV 5120->7168, O 5120->5120, gate/up 5120->2x17408 (one fused
+    Marlin tensor whose output is the [gate | up] `mixed` row) and down
+    17408->5120 through the SiLU-gated op on that `mixed` row -- the
+    production call sequence (langburst/model.py:1414-1482).  W4 g128 random
+    packed weights, all resident (about 10.9 GB)."""
+
+    HIDDEN, INTER, QKV, O_IN = 5120, 17408, 7168, 5120
+
+    def __init__(self, torch, dev, m, layers, seed):
+        gen = torch.Generator(device=dev)
+        gen.manual_seed(seed)
+        h, it = self.HIDDEN, self.INTER
+
+        def tensor(k, n):
+            q = torch.randint(-2 ** 31, 2 ** 31, (k // 16, 2 * n), dtype=torch.int32, device=dev, generator=gen)
+            s = (torch.randn((k // 128, n), device=dev, generator=gen) * 0.01).abs_().add_(1e-3).half()
+            return q, s
+
+        self.m, self.layers = m, []
+        for _ in range(layers):
+            self.layers.append({"qkv": tensor(h, self.QKV), "o": tensor(self.O_IN, h), "gate_up": tensor(h, 2 * it),
+                                "down": tensor(it, h)})
+        self.x = torch.randn((m, h), device=dev, generator=gen).half()
+        self.qkv_out = torch.empty((m, self.QKV), dtype=torch.float16, device=dev)
+        self.o_out = torch.empty((m, h), dtype=torch.float16, device=dev)
+        self.mixed = torch.randn((m, 2 * it), device=dev, generator=gen).half()  # overwritten by gate/up
+        self.down_out = torch.empty((m, h), dtype=torch.float16, device=dev)
+        self.ws = torch.zeros((2 * it // 128 * 16,), dtype=torch.int32, device=dev)
+        per_layer = (marlin_bytes(m, h, self.QKV) + marlin_bytes(m, self.O_IN, h) + marlin_bytes(m, h, 2 * it)
+                     + marlin_bytes(m, it, h) + m * it * 2)  # the gated op reads [gate | up]: 2K halves per row
+        self.bytes_per_step = per_layer * layers
+        self.weight_bytes = sum(q.numel() * 4 + s.numel() * 2 for L in self.layers for (q, s) in L.values())
+
+    def step(self, lc):
+        h, it = self.HIDDEN, self.INTER
+        for L in self.layers:
+            lc.lowbit_marlin_gemm_out(*L["qkv"], self.x, self.qkv_out, self.ws, h, 128)
+            lc.lowbit_marlin_gemm_out(*L["o"], self.x, self.o_out, self.ws, self.O_IN, 128)
+            lc.lowbit_marlin_gemm_out(*L["gate_up"], self.x, self.mixed, self.ws, h, 128)
+            lc.lowbit_marlin_gemm_silu_packed_out(*L["down"], self.mixed, self.down_out, self.ws, it, 128)
+
+
+def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5):
+    """Graph-captured decode steps (4 * layers launches each), timed with events."""
+    ds = DecodeStep(torch, dev, m, layers, seed=100 + m)
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        ds.step(lc)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        ds.step(lc)
+    graph.replay()
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record(stream)
+    for _ in range(replays):
+        graph.replay()
+    stop.record(stream)
+    torch.cuda.synchronize()
+    us = start.elapsed_time(stop) * 1e3 / replays
+    res = {"layers": layers, "launches_per_step": 4 * layers, "us_per_step": round(us, 1),
+           "bytes_per_step": ds.bytes_per_step, "weight_bytes_resident": ds.weight_bytes,
+           "GB/s": round(ds.bytes_per_step / us / 1e3, 1),
+           "frac_hbm": round(ds.bytes_per_step / us / 1e3 / HBM_PEAK_GBS, 4)}
+    del graph, ds
+    torch.cuda.empty_cache()
+    return res
+
+
 def sets_for(bytes_per_set, minimum=8):
     return max(minimum, math.ceil(2.0 * MALL_BYTES / bytes_per_set))
 
@@ -330,6 +405,9 @@ def main():
                                          "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4)}
         del pr
         torch.cuda.empty_cache()
+        for mm in (1, 32):
+            extra[f"decode_step_64_layers_m{mm}"] = r = decode_step_sweep(torch, lc, dev, mm)
+            log(f"[bench] 64-layer decode step M={mm}: {r['us_per_step']:.1f} us, {r['GB/s']:.1f} GB/s")
         result["extra"] = extra
 
     if not args.skip_cpu:

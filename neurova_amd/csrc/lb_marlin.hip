@@ -220,6 +220,10 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
     // As many k splits as fit in one wave of resident workgroups: a second,
     // partial wave would cost a whole workgroup's time for a few tiles.
     int s = (kSkinnyWGsPerCU * device_cus()) / pl.n_cg;
+    // split-K partials (S * M * N fp32, written once and read once) stay
+    // within half the weight bytes (K * N / 2): S * M <= K / 32
+    const int s_traffic = (int)std::max<int64_t>(1, k / (32 * m));
+    if (s > s_traffic) s = s_traffic;
     const int s_lds = (int)((x_all + kSkinnyMaxX - 1) / kSkinnyMaxX);
     if (s < s_lds) s = s_lds;
     if (s > groups) s = groups;
