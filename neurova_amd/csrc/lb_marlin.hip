@@ -155,7 +155,8 @@ struct Plan {
   bool skinny = true;
   int mb = 1;        // GEMM: 16-row blocks per workgroup
   int n_mb = 1;
-  int n_cg = 0;
+  int n_cg = 0;      // column tiles (decode: 64 * cpw columns; GEMM: 256)
+  int cpw = 4;       // decode: chunks (64 columns) per workgroup
   int splits = 1;    // decode: K splits of every column tile
   int full_tiles = 0;   // GEMM: tiles computed whole
   int tail_tiles = 0;   // GEMM: tiles split over K ...
@@ -172,6 +173,7 @@ struct Plan {
 #endif
 constexpr int kSkinnyWGsPerCU = LB_SKINNY_WGS_PER_CU;
 constexpr int kGemmMaxTailSplits = 16;
+constexpr int kSkinnyMaxSplits = 8;  // decode: beyond this, narrower tiles instead
 constexpr size_t kSkinnyMaxX = 48 * 1024;
 
 // Compute units of the current device (cached per device; 256 on a full MI355X,
@@ -206,32 +208,60 @@ inline int choose_tail_splits(int64_t tail, int64_t slots, int groups) {
   return best;
 }
 
+// Decode tiling with `cpw` chunks per workgroup: the k split count, or 0
+// when the tiling cannot run (some wave would get no scale group, or the
+// A slice does not fit LDS without the workspace to split K).
+inline int skinny_splits(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int cpw) {
+  const int n_cg = (int)(n / (64 * cpw));
+  const int ksub = skinny::kWaves / cpw;
+  const int groups = (int)(k / 128);
+  const size_t x_all = (size_t)k * (size_t)m * 2;
+  const bool can_split = workspace_len >= (int64_t)n_cg + 1;
+  // As many k splits as fit in one wave of resident workgroups: a second,
+  // partial wave would cost a whole workgroup's time for a few tiles.
+  int s = (kSkinnyWGsPerCU * device_cus()) / n_cg;
+  // split-K partials (S * M * N fp32, written once and read once) stay
+  // within half the weight bytes (K * N / 2): S * M <= K / 32
+  const int s_traffic = (int)std::max<int64_t>(1, k / (32 * m));
+  if (s > s_traffic) s = s_traffic;
+  // the decode kernel stages its whole A slice in LDS
+  const int s_lds = (int)((x_all + kSkinnyMaxX - 1) / kSkinnyMaxX);
+  if (s < s_lds) s = s_lds;
+  if (s > groups / ksub) s = groups / ksub;  // every wave at least one group
+  if (s < 1) s = 1;
+  if (!can_split) s = 1;
+  if (groups / s < ksub) return 0;
+  if ((size_t)((groups + s - 1) / s) * 128 * (size_t)m * 2 > kSkinnyMaxX) return 0;
+  return s;
+}
+
 // `am`: the A mode of the launch (gemm::A_PLAIN or gemm::A_SILU_PACKED).
 inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am) {
   Plan pl;
   pl.n_cg = (int)(n / 256);
   const int groups = (int)(k / 128);
-  const bool can_split = workspace_len >= (int64_t)pl.n_cg + 1;
-  const size_t x_all = (size_t)k * (size_t)m * 2;
-  // The decode kernel stages its whole A slice in LDS: without the workspace
-  // to split K, a slice too large for LDS goes to the GEMM kernel instead.
-  if (m <= skinny::kMaxM && (can_split || x_all <= kSkinnyMaxX)) {
+  // Decode: 4 chunks (one per wave) per workgroup, unless the narrow N then
+  // needs more than kSkinnyMaxSplits k splits to fill the chip: then 2 or 1
+  // chunks, whose waves share the workgroup's k range.
+  int cpw = 0, s = 0;
+  if (m <= skinny::kMaxM) {
+    for (int c = 4; c >= 1; c /= 2) {
+      const int sc = skinny_splits(m, n, k, workspace_len, c);
+      if (sc == 0) continue;
+      if (cpw == 0 || sc < s) {
+        cpw = c;
+        s = sc;
+      }
+      if (s <= kSkinnyMaxSplits) break;
+    }
+  }
+  if (cpw > 0) {
     pl.skinny = true;
-    // As many k splits as fit in one wave of resident workgroups: a second,
-    // partial wave would cost a whole workgroup's time for a few tiles.
-    int s = (kSkinnyWGsPerCU * device_cus()) / pl.n_cg;
-    // split-K partials (S * M * N fp32, written once and read once) stay
-    // within half the weight bytes (K * N / 2): S * M <= K / 32
-    const int s_traffic = (int)std::max<int64_t>(1, k / (32 * m));
-    if (s > s_traffic) s = s_traffic;
-    const int s_lds = (int)((x_all + kSkinnyMaxX - 1) / kSkinnyMaxX);
-    if (s < s_lds) s = s_lds;
-    if (s > groups) s = groups;
-    if (s < 1) s = 1;
-    if (!can_split) s = 1;
+    pl.cpw = cpw;
+    pl.n_cg = (int)(n / (64 * cpw));
     pl.splits = s;
     const int max_groups = (groups + s - 1) / s;
-    pl.x_bytes = (size_t)max_groups * 128 * (size_t)m * 2;  // staged A slice
+    pl.x_bytes = (size_t)max_groups * 128 * (size_t)m * 2;  // staged A slice (at most kSkinnyMaxX)
     // + the zero entry + the bias corrections [group][16] fp32
     const size_t stage = pl.x_bytes + 16 + (size_t)max_groups * skinny::kMaxM * 4;
     pl.lds = std::max(stage, (size_t)m * skinny::kCols * 4);
@@ -328,12 +358,20 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
     p.m = (int)m; p.n = (int)n; p.k = (int)k; p.splits = pl.splits;
     p.kp_total = (int)(k / 32); p.n_cg = pl.n_cg;
     dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
-#define LB_SK(AMV, EPV, GV) hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, EPV, GV>), grid, dim3(skinny::kThreads), pl.lds, st, p)
-#define LB_SKG(AMV, EPV) do { if (grouped) LB_SK(AMV, EPV, true); else LB_SK(AMV, EPV, false); } while (0)
+#define LB_SK(AMV, EPV, GV, CV) \
+  hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, EPV, GV, CV>), grid, dim3(skinny::kThreads), pl.lds, st, p)
+#define LB_SKC(AMV, EPV, GV)                              \
+  do {                                                    \
+    if (pl.cpw == 4) LB_SK(AMV, EPV, GV, 4);              \
+    else if (pl.cpw == 2) LB_SK(AMV, EPV, GV, 2);         \
+    else LB_SK(AMV, EPV, GV, 1);                          \
+  } while (0)
+#define LB_SKG(AMV, EPV) do { if (grouped) LB_SKC(AMV, EPV, true); else LB_SKC(AMV, EPV, false); } while (0)
     if (var == V_PLAIN) LB_SKG(skinny::A_PLAIN, skinny::EPI_STORE);
     else if (var == V_SILU) LB_SKG(skinny::A_SILU_PACKED, skinny::EPI_STORE);
     else LB_SKG(skinny::A_PLAIN, skinny::EPI_ARGMAX);
 #undef LB_SKG
+#undef LB_SKC
 #undef LB_SK
     return lbh::launch_status();
   }

@@ -12,8 +12,11 @@
 //   k = 2q+8 / 2q+9.  Group scales: the 64-column chunk of group row g stores
 //   column 8jj+i at 8i+jj, so the 8 scales a slot needs are the 16 bytes at 8c.
 //
-// Kernel.  A workgroup owns 4 chunks (256 columns) and a k range; wave w
-// streams chunk w.  The B fragment of v_mfma_f32_16x16x32_f16 (lane
+// Kernel.  A workgroup owns cpw chunks (64 * cpw columns, cpw = 4, 2 or 1)
+// and a k range; wave w streams chunk w % cpw over share w / cpw of that k
+// range (4 / cpw shares, whole scale groups), and the shares of a column are
+// added in the epilogue in share order.  cpw < 4 serves narrow N: more,
+// narrower tiles instead of many k splits.  The B fragment of v_mfma_f32_16x16x32_f16 (lane
 // l = 16g + nl holds 8 k-values of column nl) is built in registers: with
 // k-group g = (row p = g>>1, slot pair 4c+2g', 4c+2g'+1, g' = g&1) and column
 // nl = 8h + c, the fragment needs the h half of every word of both slots of
@@ -82,7 +85,7 @@ struct Params {
   int m, n, k;
   int splits;            // S
   int kp_total;          // K / 32
-  int n_cg;              // N / 256
+  int n_cg;              // N / (64 * cpw): column tiles
 };
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
@@ -128,7 +131,9 @@ __device__ __forceinline__ uint32_t silu_mul2(uint32_t g, uint32_t u) {
   return (uint32_t)f2h(silu(g0) * u0) | ((uint32_t)f2h(silu(g1) * u1) << 16);
 }
 
-template <int AM, int EPI, bool GROUPED>
+// CPW: chunks per workgroup (4, 2 or 1), a compile-time constant so that the
+// wide-N instantiation (CPW = 4) carries no k-share arithmetic.
+template <int AM, int EPI, bool GROUPED, int CPW>
 __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int s_prev;
@@ -136,16 +141,26 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int cg = blockIdx.x;  // column group (256 columns)
+  const int cg = blockIdx.x;  // column tile (64 * cpw columns)
   const int split = blockIdx.y;
   const int mrows = p.m;      // <= kMaxM
+  constexpr int cpw = CPW;
+  constexpr int ksub = kWaves / cpw;   // k shares per tile
+  const int wchunk = cpw == kWaves ? wave : (wave & (cpw - 1));  // this wave's chunk of the tile ...
+  const int wsub = cpw == kWaves ? 0 : wave / cpw;                // ... and its k share
 
   int kp0, kp1;
-  split_range(p, split, kp0, kp1);
+  split_range(p, split, kp0, kp1);  // the workgroup's k range
   const int nkp = kp1 - kp0;  // positive multiple of kSteps
+  const int ngw = nkp / kSteps;  // scale groups of the workgroup
+  // this wave's groups [gw0, gw0 + nb) of them (nb >= 1: the host plans at
+  // least ksub groups per split)
+  const int gw0 = (ngw * wsub) / ksub;
+  const int nb = (ngw * (wsub + 1)) / ksub - gw0;
+  const int kpw0 = kp0 + gw0 * kSteps;
 
   // fragment coordinates: lane = 16g + 8h + c
-  const int chunk = cg * kWaves + wave;
+  const int chunk = cg * cpw + wchunk;
   const int64_t row_words = 2 * (int64_t)p.n;  // int32 per qweight row
   const int g = lane >> 4;
   const int hsel = (lane >> 3) & 1;
@@ -214,7 +229,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
 #pragma unroll
   for (int i = 0; i < kDepth; ++i) bs[i] = (u32x4){0, 0, 0, 0};
   auto issue = [&](u32x4(&w)[kSteps], u32x4& scl, int batch) {
-    const int kpf = kp0 + batch * kSteps;
+    const int kpf = kpw0 + batch * kSteps;
 #pragma unroll
     for (int d = 0; d < kSteps; ++d) {
       const u32x4* src = reinterpret_cast<const u32x4*>(bsrc + (int64_t)(kpf + d) * 2 * row_words);
@@ -228,7 +243,6 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   };
 
   // ---- staging loads, then the first weight batches, then the stores ----
-  const int nb = nkp / kSteps;
   stage_load(0);
   __builtin_amdgcn_sched_barrier(0);  // staging loads strictly before the weight loads
 #pragma unroll
@@ -249,7 +263,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   // 1024 + 16q against x/16 (k = 8..15), i.e. x*q + 1024x and x~*q + 64x~ with
   // x~ = 16 * fp16(x/16); subtracting 1032*sum(x) + 72*sum(x~) = 1032*lo + 1152*hi
   // (sums of the staged values) leaves sum(x * (q - 8)).  Fixed-order sums.
-  for (int t = tid; GROUPED && t < nb * kMaxM; t += kThreads) {
+  for (int t = tid; GROUPED && t < ngw * kMaxM; t += kThreads) {
     const int gi = t / kMaxM, mm = t - gi * kMaxM;
     float lo = 0.f, hi = 0.f;
     if (mm < mrows) {
@@ -265,8 +279,8 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
 
   // A fragment address: rows >= M read the zero entry.
   const bool a_live = mrow < mrows;
-  const int a_base = a_live ? g * mrows + mrow : n_frag;
   const int a_step = a_live ? 4 * mrows : 0;
+  const int a_base = a_live ? g * mrows + mrow + gw0 * kSteps * a_step : n_frag;
   const int crow0 = (lane >> 4) * 4;  // accumulator rows of this lane
 
   f32x4 acc[4];
@@ -278,7 +292,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   // that sum once (per-column scales: the sum is added as is).
   auto consume = [&](const u32x4(&w)[kSteps], const u32x4& scl, int batch) {
     const f32x4 cinit =
-        GROUPED ? *reinterpret_cast<const f32x4*>(corr + batch * kMaxM + crow0) : (f32x4){0.f, 0.f, 0.f, 0.f};
+        GROUPED ? *reinterpret_cast<const f32x4*>(corr + (gw0 + batch) * kMaxM + crow0) : (f32x4){0.f, 0.f, 0.f, 0.f};
     f32x4 grp[4];
 #pragma unroll
     for (int d = 0; d < kSteps; ++d) {
@@ -351,16 +365,26 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
       }
   }
   __syncthreads();
-  const int n = cg * kCols + tid;  // this thread's output column
+  // Thread t < 64 * cpw owns column t of the tile: the sum of its k shares
+  // (the waves of chunk t / 64), in share order.
+  const bool col_live = tid < 64 * cpw;
+  const int n = cg * 64 * cpw + (col_live ? tid : 0);  // this thread's output column
   float v[kMaxM];
 #pragma unroll
-  for (int r = 0; r < kMaxM; ++r) v[r] = r < mrows ? tile[r * kCols + tid] : 0.f;
+  for (int r = 0; r < kMaxM; ++r) {
+    float t = 0.f;
+    if (r < mrows && col_live) {
+      t = tile[r * kCols + tid];  // share 0 (wave tid / 64)
+      for (int ws = 1; ws < ksub; ++ws) t += tile[r * kCols + ws * cpw * 64 + tid];
+    }
+    v[r] = t;
+  }
 
   if (p.splits > 1) {
     float* part = p.partial + (int64_t)split * p.m * p.n + n;
 #pragma unroll
     for (int r = 0; r < kMaxM; ++r)
-      if (r < mrows) publish(part + (int64_t)r * p.n, v[r]);
+      if (r < mrows && col_live) publish(part + (int64_t)r * p.n, v[r]);
     wait_published();
     __syncthreads();
     int32_t* ctr = p.counters + 1 + cg;
@@ -373,7 +397,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
     const int64_t split_stride = (int64_t)p.m * p.n;
 #pragma unroll
     for (int r0 = 0; r0 < kMaxM; r0 += 4) {
-      if (r0 < mrows) {
+      if (r0 < mrows && col_live) {
         float sum[4] = {0.f, 0.f, 0.f, 0.f};
         for (int s0 = 0; s0 < p.splits; s0 += 8) {
           float t[4][8];
@@ -396,7 +420,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
 
   // fp16 rounding (per-column scale after it, as the reference does)
   f16 colscale = (f16)1.0f;
-  if (!GROUPED) colscale = __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
+  if (!GROUPED && col_live) colscale = __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
   uint16_t outh[kMaxM];
 #pragma unroll
   for (int r = 0; r < kMaxM; ++r) {
@@ -408,7 +432,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   if (EPI == EPI_STORE) {
 #pragma unroll
     for (int r = 0; r < kMaxM; ++r)
-      if (r < mrows) p.c[(int64_t)r * p.n + n] = outh[r];
+      if (r < mrows && col_live) p.c[(int64_t)r * p.n + n] = outh[r];
     return;
   }
 
@@ -416,7 +440,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
 #pragma unroll
   for (int r = 0; r < kMaxM; ++r) {
     if (r < mrows) {
-      const uint64_t best = wave_max_u64(argmax_key(h2f(outh[r]), (uint32_t)n));
+      const uint64_t best = wave_max_u64(col_live ? argmax_key(h2f(outh[r]), (uint32_t)n) : 0ull);
       if (lane == 0) s_keys[wave][r] = best;
     }
   }

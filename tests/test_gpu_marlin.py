@@ -190,6 +190,62 @@ def test_decode_shape_cfg2(dev, m):
         assert exact > 0.95
 
 
+@pytest.mark.parametrize("m,k,n,group", [
+    (1, 5120, 5120, 128),    # 1 chunk per workgroup, 4 waves sharing each k range
+    (3, 5120, 7168, -1),
+    (16, 5120, 5120, 128),
+    (1, 17408, 5120, 128),
+    (16, 17408, 5120, 128),  # 2 chunks per workgroup (the LDS limit sets 12 splits)
+    (2, 4096, 2048, 128),
+    (5, 2560, 1024, -1),
+])
+def test_narrow_decode_vs_oracle(dev, m, k, n, group):
+    """Narrow N (the QKV / O / down projections): the decode kernel's workgroups
+    take 1 or 2 chunks and their waves share the k range; both scale modes,
+    repeated launches bit-identical."""
+    print_case("narrow", m, k, n, group)
+    codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=1300 + m + k + n)
+    got = _run_gemm(dev, x, qw, sp, group)
+    ref = O.marlin_gemm(x, qw, sp, group)
+    exact = assert_close_f16(got, ref, what=f"narrow m={m} k={k} n={n} g={group}")
+    if group <= 0:
+        assert exact > 0.9
+        _assert_per_column_rounding(got, codes, x, sp)
+    else:
+        assert_exact_scale(got, ref, O.marlin_gemm_exact(x, qw, sp, group), what=f"narrow m={m} k={k} n={n}")
+    again = _run_gemm(dev, x, qw, sp, group)
+    assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
+
+
+@pytest.mark.parametrize("m,k,n", [(1, 17408, 5120), (4, 5120, 5120)])
+def test_narrow_silu_and_argmax_vs_oracle(dev, m, k, n):
+    """The SiLU-gated and fused-argmax variants on narrow tiles."""
+    import torch
+    from neurova_amd import capi
+
+    print_case("narrow-variants", m, k, n)
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=1400 + m + k)
+    mixed = np.random.default_rng(1400 + m).normal(0, 1, (m, 2 * k)).astype(np.float16)
+    c = torch.empty((m, n), dtype=torch.float16, device=dev)
+    ws = _ws(dev, n)
+    st = capi.marlin_gemm_silu_packed(to_dev(mixed, dev), to_dev(qw, dev), c, to_dev(sp, dev), ws, 128,
+                                      _scratch(dev, m, n, k, 128))
+    assert st == 0
+    torch.cuda.synchronize()
+    assert int(ws.abs().sum()) == 0
+    assert_close_f16(to_np(c), O.marlin_gemm_silu_packed(mixed, qw, sp, k, 128), what=f"narrow silu m={m}")
+    own = _run_gemm(dev, x, qw, sp, 128).astype(np.float32)
+    state = torch.zeros((m,), dtype=torch.int64, device=dev)
+    out = torch.full((m,), -1, dtype=torch.int64, device=dev)
+    sync = torch.empty((2,), dtype=torch.int32, device=dev)
+    st = capi.marlin_gemm_argmax(to_dev(x, dev), to_dev(qw, dev), to_dev(sp, dev), ws, 128, state, out, sync, 1,
+                                 _scratch(dev, m, n, k, 128))
+    assert st == 0
+    torch.cuda.synchronize()
+    assert np.array_equal(to_np(out), own.argmax(axis=1))
+    assert int(ws.abs().sum()) == 0
+
+
 @pytest.mark.parametrize("k,n", [(5120, 17408), (17408, 5120)])
 def test_prefill_shape_cfg3(dev, k, n):
     """M=2048; a bounded row sample is checked against the oracle."""
