@@ -152,6 +152,51 @@ def test_cfg4_full_size(dev, bits, group):
     assert exact > 0.95
 
 
+@pytest.mark.parametrize("bits", [4, 8])
+def test_embedding_row_dequant_full_table(dev, bits):
+    """The embedding lookup (model.py:359-362): one row of a 248320 x 5120 table
+    per token.  The table is drawn on the GPU at full size; sampled rows (first,
+    last, interior, and out of range) are checked bit-exact against the oracle."""
+    import torch
+    import langburst_cuda as lc
+
+    rows, cols, group = 248320, 5120, 128
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(bits)
+    q = torch.randint(0, 256, (rows, cols * bits // 8), dtype=torch.uint8, device=dev, generator=gen)
+    s = (torch.randn((rows, cols // group), device=dev, generator=gen) * 0.01).abs_().add_(1e-3).half()
+    for r in (0, 1, 4097, 123456, rows - 1, rows, -3):
+        out = lc.lowbit_row_dequant(q, s, torch.tensor(r, dtype=torch.long, device=dev), cols, group, bits)
+        rr = min(max(r, 0), rows - 1)
+        ref = O.rowwise_row_dequant(to_np(q[rr:rr + 1]), to_np(s[rr:rr + 1]), 0 if 0 <= r < rows else -1, cols, group, bits)
+        assert np.array_equal(to_np(out).view(np.uint16), ref.view(np.uint16)), f"row {r}"
+
+
+@pytest.mark.parametrize("bits", [4, 8])
+@pytest.mark.parametrize("group", [64, 128])
+def test_in_proj_ba_shapes(dev, bits, group):
+    """The GDN in_proj_ba projections (model.py:227-251, 1510-1521): b and a as
+    a pair of 48-row GEMVs over K = 5120, the fused 96-row tensor as one GEMV,
+    and as a batched GEMM (MTP verification rows)."""
+    import torch
+    import langburst_cuda as lc
+
+    cols = 5120
+    _, pb, sb, x = O.make_rowwise_inputs(48, cols, bits, group, batch=3, seed=200 + bits + group)
+    _, pa, sa, _ = O.make_rowwise_inputs(48, cols, bits, group, seed=210 + bits + group)
+    qb, qa, scb, sca, xd = (to_dev(t, dev) for t in (pb, pa, sb, sa, x))
+    yb, ya = lc.lowbit_gemv_pair(qb, scb, qa, sca, xd[0], cols, group, bits)
+    assert_close_f16(to_np(yb), O.rowwise_gemv(pb, sb, x[0], cols, group, bits), what="in_proj_b")
+    assert_close_f16(to_np(ya), O.rowwise_gemv(pa, sa, x[0], cols, group, bits), what="in_proj_a")
+    pba, sba = np.concatenate([pb, pa]), np.concatenate([sb, sa])
+    qba, scba = to_dev(pba, dev), to_dev(sba, dev)
+    yba = lc.lowbit_gemv(qba, scba, xd[0], cols, group, bits)
+    torch.cuda.synchronize()
+    assert torch.equal(yba[:48], yb) and torch.equal(yba[48:], ya)
+    ym = lc.lowbit_gemm(qba, scba, xd, cols, group, bits)
+    assert_close_f16(to_np(ym), O.rowwise_gemm(pba, sba, x, cols, group, bits), what="in_proj_ba gemm")
+
+
 def test_dropin_errors(dev):
     import torch
     import langburst_cuda as lc
