@@ -294,6 +294,19 @@ def pmc_probe(torch, lc, dev, calls=24):
     log(f"[pmc-probe] {calls} headline calls, 4 copies of 256 MiB")
 
 
+def gemm_probe(torch, lc, dev, calls=6):
+    """Eager prefill GEMM calls of both BASELINE configs[2] shapes, for the
+    MFMA / clock counter runs (a few warm-up calls first)."""
+    for (k, n) in ((5120, 17408), (17408, 5120)):
+        prob = MarlinProblem(torch, dev, 2048, k, n, 1, seed=11)
+        for _ in range(calls):
+            prob.call(lc, 0)
+        torch.cuda.synchronize()
+        del prob
+        torch.cuda.empty_cache()
+    log(f"[gemm-probe] {calls} calls of each M=2048 shape")
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -304,6 +317,7 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true", help="run the counter-calibration probe and exit")
+    ap.add_argument("--gemm-probe", action="store_true", help="run the prefill GEMM counter probe and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -322,6 +336,9 @@ def main():
     torch.cuda.set_device(dev)
     if args.pmc_probe:
         pmc_probe(torch, lc, dev)
+        return
+    if args.gemm_probe:
+        gemm_probe(torch, lc, dev)
         return
     use_graph = not args.no_graph
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; graph={use_graph}")

@@ -282,6 +282,16 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
     int64_t full = (tiles / slots) * slots;
     int64_t tail = tiles - full;
     int s = tail > 0 ? choose_tail_splits(tail, slots, groups) : 1;
+    // Few rows: the kernel streams B and is bound by bandwidth, not by the
+    // MFMAs the cost model above prices; split further so that every CU gets
+    // a workgroup, as long as the fp32 partials (written and read once) stay
+    // within half the weight bytes: S <= K / (32 * tile rows).
+    if (tail > 0 && m <= 64) {
+      const int s_fill = (int)((device_cus() + tail - 1) / tail);
+      const int s_cap = (int)std::max<int64_t>(1, k / (32 * bm));
+      const int s_mem = std::min(std::min(s_fill, s_cap), groups);
+      if (s_mem > s) s = s_mem;
+    }
 #ifdef LB_GEMM_TAIL_SPLITS
     if (tail > 0) s = LB_GEMM_TAIL_SPLITS < groups ? LB_GEMM_TAIL_SPLITS : groups;
 #endif

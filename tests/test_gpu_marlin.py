@@ -246,6 +246,31 @@ def test_narrow_silu_and_argmax_vs_oracle(dev, m, k, n):
     assert int(ws.abs().sum()) == 0
 
 
+@pytest.mark.parametrize("m", [32, 48])
+def test_small_m_gemm_many_splits_vs_oracle(dev, m):
+    """M just above the decode kernel's 16 rows on the down projection (K = 17408,
+    N = 5120): few tiles, so the prefill kernel splits K many ways (13 at M = 32);
+    plain and SiLU-gated A, workspace left zero."""
+    import torch
+    from neurova_amd import capi
+
+    k, n = 17408, 5120
+    print_case("small-m-splits", m, k, n)
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=1500 + m)
+    got = _run_gemm(dev, x, qw, sp, 128)
+    exact = assert_close_f16(got, O.marlin_gemm(x, qw, sp, 128), what=f"small-m m={m}")
+    assert exact > 0.95
+    mixed = np.random.default_rng(1500 + m).normal(0, 1, (m, 2 * k)).astype(np.float16)
+    c = torch.empty((m, n), dtype=torch.float16, device=dev)
+    ws = _ws(dev, n)
+    st = capi.marlin_gemm_silu_packed(to_dev(mixed, dev), to_dev(qw, dev), c, to_dev(sp, dev), ws, 128,
+                                      _scratch(dev, m, n, k, 128))
+    assert st == 0
+    torch.cuda.synchronize()
+    assert int(ws.abs().sum()) == 0
+    assert_close_f16(to_np(c), O.marlin_gemm_silu_packed(mixed, qw, sp, k, 128), what=f"small-m silu m={m}")
+
+
 @pytest.mark.parametrize("k,n", [(5120, 17408), (17408, 5120)])
 def test_prefill_shape_cfg3(dev, k, n):
     """M=2048; a bounded row sample is checked against the oracle."""
