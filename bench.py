@@ -123,11 +123,14 @@ class DecodeStep:
     Marlin tensor whose output is the [gate | up] `mixed` row) and down
     17408->5120 through the SiLU-gated op on that `mixed` row -- the
     production call sequence (langburst/model.py:1414-1482).  W4 g128 random
-    packed weights, all resident (about 10.9 GB)."""
+    packed weights, all resident (about 10.9 GB).  fused_mlp: gate/up, SiLU
+    and down as one lb_marlin_mlp_fused call in its automatic mode (one launch
+    for M = 2..16, the two launches at M = 1), whose output is bit-identical
+    to the two calls."""
 
     HIDDEN, INTER, QKV, O_IN = 5120, 17408, 7168, 5120
 
-    def __init__(self, torch, dev, m, layers, seed):
+    def __init__(self, torch, dev, m, layers, seed, fused_mlp=False):
         gen = torch.Generator(device=dev)
         gen.manual_seed(seed)
         h, it = self.HIDDEN, self.INTER
@@ -147,6 +150,16 @@ class DecodeStep:
         self.mixed = torch.randn((m, 2 * it), device=dev, generator=gen).half()  # overwritten by gate/up
         self.down_out = torch.empty((m, h), dtype=torch.float16, device=dev)
         self.ws = torch.zeros((2 * it // 128 * 16,), dtype=torch.int32, device=dev)
+        self.fused_mlp = fused_mlp
+        self.launches_per_layer = 4
+        if fused_mlp:
+            from neurova_amd import capi
+
+            self.capi = capi
+            self.fws = torch.zeros((capi.marlin_mlp_fused_workspace_len(m, h, it),), dtype=torch.int32, device=dev)
+            self.fscratch = torch.empty((capi.marlin_mlp_fused_scratch_bytes(m, h, it),), dtype=torch.uint8,
+                                        device=dev)
+            self.launches_per_layer = 2 + capi.marlin_mlp_fused_launches(m, h, it, 128, 128)
         per_layer = (marlin_bytes(m, h, self.QKV) + marlin_bytes(m, self.O_IN, h) + marlin_bytes(m, h, 2 * it)
                      + marlin_bytes(m, it, h) + m * it * 2)  # the gated op reads [gate | up]: 2K halves per row
         self.bytes_per_step = per_layer * layers
@@ -157,13 +170,18 @@ class DecodeStep:
         for L in self.layers:
             lc.lowbit_marlin_gemm_out(*L["qkv"], self.x, self.qkv_out, self.ws, h, 128)
             lc.lowbit_marlin_gemm_out(*L["o"], self.x, self.o_out, self.ws, self.O_IN, 128)
-            lc.lowbit_marlin_gemm_out(*L["gate_up"], self.x, self.mixed, self.ws, h, 128)
-            lc.lowbit_marlin_gemm_silu_packed_out(*L["down"], self.mixed, self.down_out, self.ws, it, 128)
+            if self.fused_mlp:
+                st = self.capi.marlin_mlp_fused(self.x, *L["gate_up"], *L["down"], self.down_out, h, it, 128, 128,
+                                                self.fws, self.fscratch)
+                assert st == 0, self.capi.status_string(st)
+            else:
+                lc.lowbit_marlin_gemm_out(*L["gate_up"], self.x, self.mixed, self.ws, h, 128)
+                lc.lowbit_marlin_gemm_silu_packed_out(*L["down"], self.mixed, self.down_out, self.ws, it, 128)
 
 
-def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5):
-    """Graph-captured decode steps (4 * layers launches each), timed with events."""
-    ds = DecodeStep(torch, dev, m, layers, seed=100 + m)
+def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5, fused_mlp=False):
+    """Graph-captured decode steps (3 or 4 launches per layer), timed with events."""
+    ds = DecodeStep(torch, dev, m, layers, seed=100 + m, fused_mlp=fused_mlp)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
     with torch.cuda.stream(side):
@@ -182,7 +200,7 @@ def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5):
     stop.record(stream)
     torch.cuda.synchronize()
     us = start.elapsed_time(stop) * 1e3 / replays
-    res = {"layers": layers, "launches_per_step": 4 * layers, "us_per_step": round(us, 1),
+    res = {"layers": layers, "launches_per_step": ds.launches_per_layer * layers, "us_per_step": round(us, 1),
            "bytes_per_step": ds.bytes_per_step, "weight_bytes_resident": ds.weight_bytes,
            "GB/s": round(ds.bytes_per_step / us / 1e3, 1),
            "frac_hbm": round(ds.bytes_per_step / us / 1e3 / HBM_PEAK_GBS, 4)}
@@ -449,9 +467,13 @@ def main():
             f"embedding row {u:.2f} us")
         del emb_q, emb_s, tokens
         torch.cuda.empty_cache()
-        for mm in (1, 32):
+        for mm in (1, 4, 16, 32):
             extra[f"decode_step_64_layers_m{mm}"] = r = decode_step_sweep(torch, lc, dev, mm)
             log(f"[bench] 64-layer decode step M={mm}: {r['us_per_step']:.1f} us, {r['GB/s']:.1f} GB/s")
+        for mm in (4, 16):
+            extra[f"decode_step_64_layers_m{mm}_fused_mlp"] = r = decode_step_sweep(torch, lc, dev, mm, fused_mlp=True)
+            log(f"[bench] 64-layer decode step M={mm}, one-launch MLP: {r['us_per_step']:.1f} us, "
+                f"{r['launches_per_step']} launches")
         result["extra"] = extra
 
     if not args.skip_cpu:

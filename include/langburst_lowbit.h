@@ -155,6 +155,35 @@ int lb_marlin_mlp_streaming(const int32_t* gate_up_qweight, const uint16_t* gate
                             int64_t gate_group_size, int64_t down_group_size,
                             void* scratch, size_t scratch_bytes, lb_stream_t stream);
 
+/* Decode MLP: out[batch, hidden] = down(fp16(silu(g) * u)) with
+ * [g | u] = fp16(gate_up(x)); gate_up is a Marlin tensor [hidden -> 2*intermediate]
+ * (gate = first half), down is [intermediate -> hidden].  The numerics of the
+ * reference's production MLP, which runs the gate_up projection and then
+ * down.gemm_silu_packed as two launches (adapters/qwen36_impl/model.py:1460-1470
+ * _fused_marlin_down, loader.py:337-368): bit-identical to lb_marlin_gemm followed
+ * by lb_marlin_gemm_silu_packed, in every mode.
+ * No reference op: replaces that pair of calls.
+ * mode: 0 auto (one launch for batch 2..16 when every workgroup of it fits on
+ *       the device at once, else the two launches), 1 one launch whenever it
+ *       fits, 2 always the two launches.  lb_marlin_mlp_fused_launches says
+ *       which a call takes.
+ * workspace: int32 [lb_marlin_mlp_fused_workspace_len()], zero on entry, left
+ *            zero (entry 1 stays 1 if a hand-off wait gave up: the
+ *            output is then not valid).
+ * scratch:   lb_marlin_mlp_fused_scratch_bytes() bytes, 256-byte aligned.
+ * Calls that share a workspace must not overlap. */
+size_t lb_marlin_mlp_fused_scratch_bytes(int64_t batch, int64_t hidden, int64_t intermediate);
+int64_t lb_marlin_mlp_fused_workspace_len(int64_t batch, int64_t hidden, int64_t intermediate);
+/* 1 (one launch), 2 (two launches), 0 (batch 0) or -status for an unsupported problem or mode. */
+int lb_marlin_mlp_fused_launches(int64_t batch, int64_t hidden, int64_t intermediate,
+                                 int64_t gate_group_size, int64_t down_group_size, int32_t mode);
+int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qweight, const uint16_t* gate_up_scales,
+                        const int32_t* down_qweight, const uint16_t* down_scales, uint16_t* out,
+                        int64_t batch, int64_t hidden, int64_t intermediate,
+                        int64_t gate_group_size, int64_t down_group_size, int32_t mode,
+                        int32_t* workspace, int64_t workspace_len,
+                        void* scratch, size_t scratch_bytes, lb_stream_t stream);
+
 /* Dense fp16 W[N, K] = fp16((q - 8) * s) (or q - 8 for per-column scales),
  * bit-exact with the reference's in-kernel dequant (csrc/marlin_cuda_kernel.cu:131-159).
  * No reference counterpart as an op: the inverse of the layout is the

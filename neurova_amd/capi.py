@@ -44,6 +44,10 @@ _SIGNATURES = {
     "lb_marlin_mlp_scratch_bytes": ([I64, I64, I64], SZ),
     "lb_marlin_mlp_streaming": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, SZ, P], ctypes.c_int),
     "lb_marlin_dequant": ([P, P, P, I64, I64, I64, P], ctypes.c_int),
+    "lb_marlin_mlp_fused_scratch_bytes": ([I64, I64, I64], SZ),
+    "lb_marlin_mlp_fused_workspace_len": ([I64, I64, I64], I64),
+    "lb_marlin_mlp_fused_launches": ([I64, I64, I64, I64, I64, I32], ctypes.c_int),
+    "lb_marlin_mlp_fused": ([P, P, P, P, P, P, I64, I64, I64, I64, I64, I32, P, I64, P, SZ, P], ctypes.c_int),
 }
 
 
@@ -144,6 +148,29 @@ def marlin_mlp_streaming(gu_q, gu_s, d_q, d_s, x, out, accum, sync, hidden, inte
     return lib().lb_marlin_mlp_streaming(_ptr(gu_q), _ptr(gu_s), _ptr(d_q), _ptr(d_s), _ptr(x), _ptr(out),
                                          _ptr(accum), _ptr(sync), x.shape[0], hidden, intermediate, gg, dg,
                                          _ptr(scratch), nbytes, _stream(x))
+
+
+def marlin_mlp_fused_scratch_bytes(batch, hidden, intermediate) -> int:
+    return int(lib().lb_marlin_mlp_fused_scratch_bytes(batch, hidden, intermediate))
+
+
+def marlin_mlp_fused_workspace_len(batch, hidden, intermediate) -> int:
+    return int(lib().lb_marlin_mlp_fused_workspace_len(batch, hidden, intermediate))
+
+
+MLP_AUTO, MLP_ONE_LAUNCH, MLP_TWO_LAUNCHES = 0, 1, 2
+
+
+def marlin_mlp_fused_launches(batch, hidden, intermediate, gg, dg, mode=MLP_AUTO) -> int:
+    return int(lib().lb_marlin_mlp_fused_launches(batch, hidden, intermediate, gg, dg, mode))
+
+
+def marlin_mlp_fused(x, gu_q, gu_s, d_q, d_s, out, hidden, intermediate, gg, dg, workspace, scratch,
+                     mode=MLP_AUTO) -> int:
+    nbytes = scratch.numel() * scratch.element_size()
+    return lib().lb_marlin_mlp_fused(_ptr(x), _ptr(gu_q), _ptr(gu_s), _ptr(d_q), _ptr(d_s), _ptr(out), x.shape[0],
+                                     hidden, intermediate, gg, dg, mode, _ptr(workspace), workspace.numel(),
+                                     _ptr(scratch), nbytes, _stream(x))
 
 
 def marlin_dequant(b, s, w_nk, k, group_size) -> int:

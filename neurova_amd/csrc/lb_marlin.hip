@@ -1,12 +1,15 @@
 // Host dispatch and C-ABI entry points for the Marlin-layout W4A16 path:
 // GEMM (decode and prefill kernels), SiLU-gated A prologue, fused argmax,
-// dense dequant and the streaming MLP.
+// dense dequant, the streaming MLP and the one-launch decode MLP.
 
 #include <stdlib.h>
 
 #include <algorithm>
 
+#include <mutex>
+
 #include "marlin_gemm.hpp"
+#include "marlin_mlp.hpp"
 #include "marlin_skinny.hpp"
 
 namespace lb {
@@ -554,5 +557,197 @@ extern "C" int lb_marlin_mlp_streaming(const int32_t* gate_up_qweight, const uin
   const int64_t no = batch * hidden;
   hipLaunchKernelGGL(marlin::f32_finalize_kernel, dim3((unsigned)((no + 255) / 256)), dim3(256), 0, st, dp, out, no,
                      pl.s2);
+  return lbh::launch_status();
+}
+
+// ---------------------------------------------------------------------------
+// Decode MLP in one launch (marlin_mlp.hpp)
+// ---------------------------------------------------------------------------
+namespace {
+struct FusedMlpPlan {
+  marlin::Plan up, down;  // the separate projections' tilings
+  bool one_launch = false;
+  int wgs = 0;
+  size_t lds = 0;
+  size_t up_partial = 0, act = 0, down_partial = 0;  // scratch offsets
+  size_t mixed = 0;                                  // two-launch form: [g | u] fp16
+  size_t scratch = 0;      // bytes this launch uses
+  size_t scratch_max = 0;  // bytes either form uses
+  int64_t ws_up = 0, ws_down = 0, ws_len = 0;        // workspace offsets, length
+};
+
+using FusedKernel = void (*)(mlp::FusedParams);
+
+template <bool G1, bool G2>
+FusedKernel fused_kernel_g(int cpw1, int cpw2) {
+  if (cpw1 == 4) {
+    if (cpw2 == 4) return mlp::marlin_mlp_fused_kernel<G1, 4, G2, 4>;
+    if (cpw2 == 2) return mlp::marlin_mlp_fused_kernel<G1, 4, G2, 2>;
+    return mlp::marlin_mlp_fused_kernel<G1, 4, G2, 1>;
+  }
+  if (cpw2 == 4) return mlp::marlin_mlp_fused_kernel<G1, 2, G2, 4>;
+  if (cpw2 == 2) return mlp::marlin_mlp_fused_kernel<G1, 2, G2, 2>;
+  return mlp::marlin_mlp_fused_kernel<G1, 2, G2, 1>;
+}
+
+FusedKernel fused_kernel(bool g1, bool g2, int cpw1, int cpw2) {
+  if (g1) return g2 ? fused_kernel_g<true, true>(cpw1, cpw2) : fused_kernel_g<true, false>(cpw1, cpw2);
+  return g2 ? fused_kernel_g<false, true>(cpw1, cpw2) : fused_kernel_g<false, false>(cpw1, cpw2);
+}
+
+// Workgroups of `fn` resident per CU with `lds` bytes of dynamic LDS, cached.
+int resident_per_cu(FusedKernel fn, size_t lds) {
+  struct Entry { FusedKernel fn; size_t lds; int dev; int v; };
+  static std::mutex mu;
+  static Entry cache[64];
+  static int used = 0;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 0;
+  std::lock_guard<std::mutex> lock(mu);
+  for (int i = 0; i < used; ++i)
+    if (cache[i].fn == fn && cache[i].lds == lds && cache[i].dev == dev) return cache[i].v;
+  int v = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, reinterpret_cast<const void*>(fn), skinny::kThreads, lds) !=
+      hipSuccess)
+    v = 0;
+  if (used < 64) cache[used++] = Entry{fn, lds, dev, v};
+  return v;
+}
+
+// Launch modes of lb_marlin_mlp_fused.  Auto: one launch from batch 2 on (at
+// batch 1 the fused kernel measured no faster than the two launches in a
+// graph-captured decode step; from batch 4 on it is, as its down phase stages
+// plain activations instead of SiLU-gating [g | u]).
+enum { kMlpAuto = 0, kMlpOne = 1, kMlpTwo = 2 };
+
+// occupancy == false: plan the layouts only (no device query; two launches).
+FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g1, bool g2, int mode,
+                            bool occupancy = true) {
+  FusedMlpPlan p;
+  p.up = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN);
+  p.down = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED);
+  const bool wanted = mode == kMlpOne || (mode == kMlpAuto && batch >= 2);
+  if (p.up.skinny && p.up.cpw >= 2 && p.down.skinny && p.down.splits <= mlp::kMaxSplits) {
+    p.wgs = std::max(p.up.n_cg * p.up.splits, p.down.n_cg * p.down.splits);
+    p.lds = std::max(p.up.lds, p.down.lds);
+    if (occupancy && wanted) {
+      const int per_cu = resident_per_cu(fused_kernel(g1, g2, p.up.cpw, p.down.cpw), p.lds);
+      p.one_launch = (int64_t)p.wgs <= (int64_t)per_cu * marlin::device_cus();
+    }
+  }
+  // one launch: gate_up partials | activations [batch][inter] fp16 | down partials
+  const size_t up_off = 0;
+  const size_t act_off = up_off + p.up.partial_bytes;
+  const size_t down_off = act_off + marlin::align_up((size_t)batch * (size_t)inter * 2);
+  const size_t one_bytes = down_off + p.down.partial_bytes;
+  // two launches: [g | u] fp16, then either projection's own scratch
+  const size_t after = marlin::align_up((size_t)batch * (size_t)(2 * inter) * 2);
+  const size_t two_bytes = after + std::max(lb_marlin_scratch_bytes(batch, 2 * inter, hidden, 128),
+                                            lb_marlin_scratch_bytes(batch, hidden, inter, 128));
+  p.scratch_max = std::max(one_bytes, two_bytes);
+  if (p.one_launch) {
+    p.up_partial = up_off;
+    p.act = act_off;
+    p.down_partial = down_off;
+    p.scratch = one_bytes;
+  } else {
+    p.mixed = 0;
+    p.up_partial = p.down_partial = after;
+    p.scratch = two_bytes;
+  }
+  // workspace: the hand-off counters and fault flag, then each projection's counters
+  p.ws_up = mlp::kSyncWorkspace;
+  p.ws_down = p.ws_up + 1 + std::max<int64_t>(p.up.n_cg, p.up.tail_tiles);
+  p.ws_len = p.ws_down + 1 + std::max<int64_t>(p.down.n_cg, p.down.tail_tiles);
+  return p;
+}
+
+int fused_mlp_check(int64_t batch, int64_t hidden, int64_t inter, int64_t gate_group, int64_t down_group, int& g1,
+                    int& g2) {
+  if (batch < 0 || hidden <= 0 || inter <= 0) return LB_ERR_ARG;
+  if (hidden % 256 || inter % 128) return LB_ERR_PROB_SHAPE;
+  if (batch > 65535LL * 128 || hidden > (1LL << 30) || inter > (1LL << 29)) return LB_ERR_ARG;
+  if (marlin::normalize_group(gate_group, hidden, g1) != LB_OK) return LB_ERR_PROB_SHAPE;
+  if (marlin::normalize_group(down_group, inter, g2) != LB_OK) return LB_ERR_PROB_SHAPE;
+  return LB_OK;
+}
+}  // namespace
+
+extern "C" size_t lb_marlin_mlp_fused_scratch_bytes(int64_t batch, int64_t hidden, int64_t intermediate) {
+  int g1 = 0, g2 = 0;
+  if (batch <= 0 || fused_mlp_check(batch, hidden, intermediate, 128, 128, g1, g2) != LB_OK) return 0;
+  return fused_mlp_plan(batch, hidden, intermediate, true, true, kMlpTwo, false).scratch_max;
+}
+
+extern "C" int64_t lb_marlin_mlp_fused_workspace_len(int64_t batch, int64_t hidden, int64_t intermediate) {
+  int g1 = 0, g2 = 0;
+  if (batch <= 0 || fused_mlp_check(batch, hidden, intermediate, 128, 128, g1, g2) != LB_OK) return 0;
+  return fused_mlp_plan(batch, hidden, intermediate, true, true, kMlpTwo, false).ws_len;
+}
+
+extern "C" int lb_marlin_mlp_fused_launches(int64_t batch, int64_t hidden, int64_t intermediate,
+                                            int64_t gate_group_size, int64_t down_group_size, int32_t mode) {
+  int g1 = 0, g2 = 0;
+  const int st = fused_mlp_check(batch, hidden, intermediate, gate_group_size, down_group_size, g1, g2);
+  if (st != LB_OK) return -st;
+  if (mode < kMlpAuto || mode > kMlpTwo) return -LB_ERR_ARG;
+  if (batch == 0) return 0;
+  return fused_mlp_plan(batch, hidden, intermediate, g1, g2, mode).one_launch ? 1 : 2;
+}
+
+extern "C" int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qweight, const uint16_t* gate_up_scales,
+                                   const int32_t* down_qweight, const uint16_t* down_scales, uint16_t* out,
+                                   int64_t batch, int64_t hidden, int64_t intermediate, int64_t gate_group_size,
+                                   int64_t down_group_size, int32_t mode, int32_t* workspace, int64_t workspace_len,
+                                   void* scratch, size_t scratch_bytes, lb_stream_t stream) {
+  int g1 = 0, g2 = 0;
+  const int st0 = fused_mlp_check(batch, hidden, intermediate, gate_group_size, down_group_size, g1, g2);
+  if (st0 != LB_OK) return st0;
+  if (mode < kMlpAuto || mode > kMlpTwo) return LB_ERR_ARG;
+  if (batch == 0) return LB_OK;
+  if (!x || !gate_up_qweight || !gate_up_scales || !down_qweight || !down_scales || !out || !workspace)
+    return LB_ERR_ARG;
+  if (!lbh::aligned(x, 16) || !lbh::aligned(gate_up_qweight, 16) || !lbh::aligned(gate_up_scales, 16) ||
+      !lbh::aligned(down_qweight, 16) || !lbh::aligned(down_scales, 16) || !lbh::aligned(out, 2))
+    return LB_ERR_ALIGN;
+  const FusedMlpPlan pl = fused_mlp_plan(batch, hidden, intermediate, g1, g2, mode);
+  if (workspace_len < pl.ws_len) return LB_ERR_WORKSPACE;
+  if (!scratch || scratch_bytes < pl.scratch) return LB_ERR_SCRATCH;
+  if (!lbh::aligned(scratch, 256)) return LB_ERR_ALIGN;
+  unsigned char* sc = reinterpret_cast<unsigned char*>(scratch);
+  hipStream_t st = (hipStream_t)stream;
+  const int64_t n_up = 2 * intermediate;
+
+  if (!pl.one_launch) {
+    uint16_t* mixed = reinterpret_cast<uint16_t*>(sc + pl.mixed);
+    const size_t rest = scratch_bytes - pl.up_partial;
+    int e = marlin::run(marlin::V_PLAIN, x, gate_up_qweight, mixed, gate_up_scales, batch, n_up, hidden,
+                        workspace + pl.ws_up, workspace_len - pl.ws_up, gate_group_size, nullptr, nullptr,
+                        sc + pl.up_partial, rest, st);
+    if (e != LB_OK) return e;
+    return marlin::run(marlin::V_SILU, mixed, down_qweight, out, down_scales, batch, hidden, intermediate,
+                       workspace + pl.ws_down, workspace_len - pl.ws_down, down_group_size, nullptr, nullptr,
+                       sc + pl.down_partial, rest, st);
+  }
+
+  mlp::FusedParams f{};
+  skinny::Params& u = f.up;
+  u.a = x; u.b = reinterpret_cast<const uint32_t*>(gate_up_qweight); u.s = gate_up_scales; u.c = nullptr;
+  u.counters = workspace + pl.ws_up;
+  u.partial = pl.up.partial_bytes ? reinterpret_cast<float*>(sc + pl.up_partial) : nullptr;
+  u.m = (int)batch; u.n = (int)n_up; u.k = (int)hidden; u.splits = pl.up.splits;
+  u.kp_total = (int)(hidden / 32); u.n_cg = pl.up.n_cg;
+  u.act_out = reinterpret_cast<uint32_t*>(sc + pl.act);
+  u.gate_chunks = (int)(intermediate / 64);
+  skinny::Params& d = f.down;
+  d.a = reinterpret_cast<const uint16_t*>(sc + pl.act);
+  d.b = reinterpret_cast<const uint32_t*>(down_qweight); d.s = down_scales; d.c = out;
+  d.counters = workspace + pl.ws_down;
+  d.partial = pl.down.partial_bytes ? reinterpret_cast<float*>(sc + pl.down_partial) : nullptr;
+  d.m = (int)batch; d.n = (int)hidden; d.k = (int)intermediate; d.splits = pl.down.splits;
+  d.kp_total = (int)(intermediate / 32); d.n_cg = pl.down.n_cg;
+  f.ws = workspace;
+  hipLaunchKernelGGL(fused_kernel(g1, g2, pl.up.cpw, pl.down.cpw), dim3((unsigned)pl.wgs), dim3(skinny::kThreads),
+                     pl.lds, st, f);
   return lbh::launch_status();
 }

@@ -78,11 +78,8 @@ __device__ __forceinline__ uint64_t shfl_xor_u64(uint64_t v, int lane, int off) 
   return ((uint64_t)hi << 32) | lo;
 }
 
-// Raw buffer resource (gfx9 V#: stride 0, 32-bit data format).  Loads at or
-// past num_records return zero: rows of the last M block beyond M use that.
-__device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, uint32_t bytes) {
-  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, 0x00020000);
-}
+// buffer_of (lb_common.hpp): loads at or past num_records return zero; rows
+// of the last M block beyond M use that.
 
 constexpr int kSteps = 4;  // 32-k steps per stage (one scale group of 128)
 

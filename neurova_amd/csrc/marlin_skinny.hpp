@@ -69,8 +69,12 @@ constexpr int kDepth = LB_SKINNY_DEPTH;  // weight batches in flight
 #define LB_STREAM_LOADS 0               // non-temporal weight loads (measured slower)
 #endif
 
-enum AMode { A_PLAIN = 0, A_SILU_PACKED = 1 };
-enum EpiMode { EPI_STORE = 0, EPI_ARGMAX = 1 };
+// A_HANDOFF: plain fp16 A written earlier in the same launch by other
+// workgroups (the fused MLP's activations), read with device-coherent loads.
+enum AMode { A_PLAIN = 0, A_SILU_PACKED = 1, A_HANDOFF = 2 };
+// EPI_ACT: the tile pairs gate and up chunks (gate_up projection of an MLP)
+// and stores fp16(silu(g) * u) of its fp16 outputs instead of the outputs.
+enum EpiMode { EPI_STORE = 0, EPI_ARGMAX = 1, EPI_ACT = 2 };
 
 struct Params {
   const uint16_t* a;     // x [M, K] (A_PLAIN) or mixed [M, 2K] (A_SILU_PACKED)
@@ -86,6 +90,8 @@ struct Params {
   int splits;            // S
   int kp_total;          // K / 32
   int n_cg;              // N / (64 * cpw): column tiles
+  uint32_t* act_out;     // EPI_ACT: fp16 pairs [M][N / 4] (N / 2 neurons)
+  int gate_chunks;       // EPI_ACT: N / 128, chunks of the gate half
 };
 
 __device__ __forceinline__ float silu(float v) { return v / (1.0f + __expf(-v)); }
@@ -131,18 +137,39 @@ __device__ __forceinline__ uint32_t silu_mul2(uint32_t g, uint32_t u) {
   return (uint32_t)f2h(silu(g0) * u0) | ((uint32_t)f2h(silu(g1) * u1) << 16);
 }
 
-// CPW: chunks per workgroup (4, 2 or 1), a compile-time constant so that the
-// wide-N instantiation (CPW = 4) carries no k-share arithmetic.
-template <int AM, int EPI, bool GROUPED, int CPW>
-__global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
+// Global chunk (64 columns) of chunk c (0 .. CPW-1) of column tile cg.  EPI_ACT
+// pairs the gate and up halves of a gate_up projection: chunks 0 .. CPW/2-1
+// are gate chunks, the rest the up chunks of the same neurons.
+template <int EPI, int CPW>
+__device__ __forceinline__ int tile_chunk(const Params& p, int cg, int c) {
+  if (EPI == EPI_ACT) {
+    constexpr int h = CPW / 2;
+    return c < h ? cg * h + c : p.gate_chunks + cg * h + (c - h);
+  }
+  return cg * CPW + c;
+}
+
+struct NoWait {
+  __device__ void operator()() const {}
+};
+
+// One workgroup's share of the projection: column tile cg (64 * CPW columns),
+// k split `split`.  CPW: chunks per workgroup (4, 2 or 1), a compile-time
+// constant so that the wide-N instantiation (CPW = 4) carries no k-share
+// arithmetic.  Uses the kernel's dynamic LDS.  A_HANDOFF: the first weight
+// batches are fetched, then `wait_for_a()` (every thread calls it) waits
+// until A has been written, then A is staged.  Returns true in the workgroup
+// that stored the tile's outputs (EPI_STORE, EPI_ACT) or ran the launch's
+// final argmax reduction.
+template <int AM, int EPI, bool GROUPED, int CPW, typename WaitA = NoWait>
+__device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const int split, WaitA wait_for_a = WaitA()) {
+  static_assert(EPI != EPI_ACT || CPW >= 2, "EPI_ACT pairs a gate and an up chunk");
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int s_prev;
   __shared__ uint64_t s_keys[kWaves][kMaxM];
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int cg = blockIdx.x;  // column tile (64 * cpw columns)
-  const int split = blockIdx.y;
   const int mrows = p.m;      // <= kMaxM
   constexpr int cpw = CPW;
   constexpr int ksub = kWaves / cpw;   // k shares per tile
@@ -160,7 +187,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   const int kpw0 = kp0 + gw0 * kSteps;
 
   // fragment coordinates: lane = 16g + 8h + c
-  const int chunk = cg * cpw + wchunk;
+  const int chunk = EPI == EPI_ACT ? tile_chunk<EPI, CPW>(p, cg, wchunk) : cg * cpw + wchunk;
   const int64_t row_words = 2 * (int64_t)p.n;  // int32 per qweight row
   const int g = lane >> 4;
   const int hsel = (lane >> 3) & 1;
@@ -188,6 +215,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   const int n_frag = nkp * 4 * mrows;  // staged entries; afr[n_frag] is the zero entry
   float* corr = reinterpret_cast<float*>(afr + n_frag + 1);
   const int64_t a_row_stride = AM == A_SILU_PACKED ? 2 * (int64_t)p.k : (int64_t)p.k;
+  const __amdgpu_buffer_rsrc_t ra = buffer_of(p.a, (uint32_t)((int64_t)mrows * p.k * 2));  // A_HANDOFF
   uint4 gv[kStageUnroll], uv[kStageUnroll];
   auto stage_load = [&](int base) __attribute__((always_inline)) {
 #pragma unroll
@@ -195,7 +223,10 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
       const int it = min(base + u * kThreads + tid, items - 1);
       const int mm = it / octs;
       const uint16_t* src = p.a + (int64_t)mm * a_row_stride + k0 + ((it - mm * octs) << 3);
-      gv[u] = *reinterpret_cast<const uint4*>(src);
+      if (AM == A_HANDOFF)
+        gv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, (uint32_t)(src - p.a) * 2u, 0, kSc1));
+      else
+        gv[u] = *reinterpret_cast<const uint4*>(src);
       if (AM == A_SILU_PACKED) uv[u] = *reinterpret_cast<const uint4*>(src + p.k);
     }
   };
@@ -243,12 +274,17 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   };
 
   // ---- staging loads, then the first weight batches, then the stores ----
-  stage_load(0);
+  // (A_HANDOFF: the weight batches first, then the wait for A)
+  if (AM != A_HANDOFF) stage_load(0);
   __builtin_amdgcn_sched_barrier(0);  // staging loads strictly before the weight loads
 #pragma unroll
   for (int i = 0; i < kDepth; ++i) {
     issue(bw[i], bs[i], min(i, nb - 1));
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: the loop's waits assume it
+  }
+  if (AM == A_HANDOFF) {
+    wait_for_a();
+    stage_load(0);
   }
   __builtin_amdgcn_sched_barrier(0);
   stage_store(0);
@@ -368,7 +404,9 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   // Thread t < 64 * cpw owns column t of the tile: the sum of its k shares
   // (the waves of chunk t / 64), in share order.
   const bool col_live = tid < 64 * cpw;
-  const int n = cg * 64 * cpw + (col_live ? tid : 0);  // this thread's output column
+  // this thread's output column
+  const int n = EPI == EPI_ACT ? (col_live ? tile_chunk<EPI, CPW>(p, cg, tid >> 6) * 64 + (tid & 63) : 0)
+                               : cg * 64 * cpw + (col_live ? tid : 0);
   float v[kMaxM];
 #pragma unroll
   for (int r = 0; r < kMaxM; ++r) {
@@ -390,7 +428,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
     int32_t* ctr = p.counters + 1 + cg;
     if (tid == 0) s_prev = arrive(ctr);
     __syncthreads();
-    if (s_prev != p.splits - 1) return;  // not the last split of this tile
+    if (s_prev != p.splits - 1) return false;  // not the last split of this tile
     if (tid == 0) reset_counter(ctr);
     // Sum the partials in split order; 4 rows x 8 splits of reads in flight.
     const float* src = p.partial + n;
@@ -433,7 +471,28 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
 #pragma unroll
     for (int r = 0; r < kMaxM; ++r)
       if (r < mrows && col_live) p.c[(int64_t)r * p.n + n] = outh[r];
-    return;
+    return true;
+  }
+
+  if (EPI == EPI_ACT) {
+    // The tile's fp16 outputs [mrows][64 * CPW] (gate half, then up half) go
+    // through LDS; thread t then forms neuron pair t of a row with the same
+    // SiLU-gated product as the A_SILU_PACKED staging and publishes it.
+    constexpr int kTileCols = 64 * CPW, kPairs = 16 * CPW;  // neuron pairs per row
+    uint16_t* xch = reinterpret_cast<uint16_t*>(smem);
+    __syncthreads();  // every thread is done with the fp32 tile
+#pragma unroll
+    for (int r = 0; r < kMaxM; ++r)
+      if (r < mrows && col_live) xch[r * kTileCols + tid] = outh[r];
+    __syncthreads();
+    const uint32_t* xw = reinterpret_cast<const uint32_t*>(xch);
+    for (int it = tid; it < mrows * kPairs; it += kThreads) {
+      const int r = it / kPairs, t = it - r * kPairs;
+      const uint32_t gw = xw[r * (kTileCols / 2) + t];
+      const uint32_t uw = xw[r * (kTileCols / 2) + kPairs + t];
+      publish(p.act_out + (int64_t)r * (p.n / 4) + (int64_t)cg * kPairs + t, silu_mul2(gw, uw));
+    }
+    return true;
   }
 
   // ---- argmax: per-row max over this tile's 256 columns, then over tiles ----
@@ -456,7 +515,7 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
   int32_t* final_counter = p.counters;
   if (tid == 0) s_prev = arrive(final_counter);
   __syncthreads();
-  if (s_prev != p.n_cg - 1) return;
+  if (s_prev != p.n_cg - 1) return false;
   if (tid == 0) reset_counter(final_counter);
   for (int r = wave; r < mrows; r += kWaves) {
     uint64_t best = 0;
@@ -467,6 +526,12 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
       p.argmax_out[r] = (int64_t)(0xffffffffu - (uint32_t)(best & 0xffffffffu));
     }
   }
+  return true;
+}
+
+template <int AM, int EPI, bool GROUPED, int CPW>
+__global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
+  skinny_tile<AM, EPI, GROUPED, CPW>(p, blockIdx.x, blockIdx.y);
 }
 
 }  // namespace skinny

@@ -1,0 +1,146 @@
+"""The one-launch decode MLP (``lb_marlin_mlp_fused``) against the two
+projections it fuses, and against the oracle.
+
+The reference runs its production MLP as the gate_up projection followed by
+``down.gemm_silu_packed`` (``adapters/qwen36_impl/model.py:1460-1470``,
+``loader.py:337-368``).  The fused entry point must return exactly what
+``lb_marlin_gemm`` followed by ``lb_marlin_gemm_silu_packed`` return (with a
+workspace large enough that both plan the same tilings), leave its workspace
+zero, and meet the parity bar (tests/gpu_util.py) against the oracle's
+dequant-then-matmul of the same two steps.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from oracle import lowbit_oracle as O
+from tests.gpu_util import assert_close_f16, print_case, to_dev, to_np
+
+pytestmark = pytest.mark.gpu
+
+HIDDEN, INTER = 5120, 17408  # the model's MLP (BASELINE.json cfg5)
+
+
+def _problem(hidden, inter, batch, gg, dg, seed):
+    rng = np.random.default_rng(seed)
+    gu_codes = rng.integers(0, 16, size=(hidden, 2 * inter), dtype=np.uint8)
+    d_codes = rng.integers(0, 16, size=(inter, hidden), dtype=np.uint8)
+    gu_groups = 1 if gg == -1 else hidden // 128
+    d_groups = 1 if dg == -1 else inter // 128
+    # per-column scales apply after the fp16 rounding: keep those outputs in range
+    gu_s = (np.abs(rng.normal(0, 0.01, (gu_groups, 2 * inter))) + 1e-3).astype(np.float16)
+    d_s = (np.abs(rng.normal(0, 0.01, (d_groups, hidden))) + 1e-3).astype(np.float16)
+    x = rng.normal(0, 1, (batch, hidden)).astype(np.float16)
+    return (O.marlin_pack_codes(gu_codes), O.marlin_pack_scales(gu_s, per_column=gg == -1),
+            O.marlin_pack_codes(d_codes), O.marlin_pack_scales(d_s, per_column=dg == -1), x)
+
+
+def _problem_dev(hidden, inter, batch, seed, dev):
+    """Model-sized problem drawn on the GPU: every int32 pattern is a valid
+    Marlin tensor (8 codes per word), scales |N(0, 0.01)| + 1e-3."""
+    import torch
+
+    g = torch.Generator(device=dev)
+    g.manual_seed(seed)
+    gu_q = torch.randint(-2**31, 2**31, (hidden // 16, 4 * inter), dtype=torch.int32, device=dev, generator=g)
+    d_q = torch.randint(-2**31, 2**31, (inter // 16, 2 * hidden), dtype=torch.int32, device=dev, generator=g)
+    gu_s = (torch.randn((hidden // 128, 2 * inter), device=dev, generator=g) * 0.01).abs_().add_(1e-3).half()
+    d_s = (torch.randn((inter // 128, hidden), device=dev, generator=g) * 0.01).abs_().add_(1e-3).half()
+    x = torch.randn((batch, hidden), device=dev, generator=g).half()
+    return [x, gu_q, gu_s, d_q, d_s]
+
+
+def _two_launches(dev, x, gu_q, gu_s, d_q, d_s, hidden, inter, gg, dg):
+    import torch
+    from neurova_amd import capi
+
+    batch = x.shape[0]
+    mixed = torch.empty((batch, 2 * inter), dtype=torch.float16, device=dev)
+    out = torch.empty((batch, hidden), dtype=torch.float16, device=dev)
+    ws = torch.zeros((1 << 14,), dtype=torch.int32, device=dev)
+    s1 = torch.empty((max(1, capi.marlin_scratch_bytes(batch, 2 * inter, hidden, gg)),), dtype=torch.uint8, device=dev)
+    s2 = torch.empty((max(1, capi.marlin_scratch_bytes(batch, hidden, inter, dg)),), dtype=torch.uint8, device=dev)
+    assert capi.marlin_gemm(x, gu_q, mixed, gu_s, ws, gg, s1) == 0
+    assert capi.marlin_gemm_silu_packed(mixed, d_q, out, d_s, ws, dg, s2) == 0
+    torch.cuda.synchronize()
+    return to_np(out), to_np(mixed)
+
+
+def _fused(dev, x, gu_q, gu_s, d_q, d_s, hidden, inter, gg, dg, ws=None, mode=1):
+    import torch
+    from neurova_amd import capi
+
+    batch = x.shape[0]
+    out = torch.full((batch, hidden), float("nan"), dtype=torch.float16, device=dev)
+    if ws is None:
+        ws = torch.zeros((capi.marlin_mlp_fused_workspace_len(batch, hidden, inter),), dtype=torch.int32, device=dev)
+    scratch = torch.empty((capi.marlin_mlp_fused_scratch_bytes(batch, hidden, inter),), dtype=torch.uint8,
+                          device=dev)
+    st = capi.marlin_mlp_fused(x, gu_q, gu_s, d_q, d_s, out, hidden, inter, gg, dg, ws, scratch, mode=mode)
+    assert st == 0, capi.status_string(st)
+    torch.cuda.synchronize()
+    assert int(ws.abs().sum()) == 0, f"workspace not left zero: {ws.nonzero().flatten()[:8].tolist()}"
+    return to_np(out)
+
+
+CASES = [
+    # hidden, inter, batch, gate group, down group
+    (512, 1024, 1, 128, 128),
+    (512, 1024, 3, 128, 128),
+    (768, 1536, 16, 128, 128),
+    (512, 1024, 2, -1, 128),
+    (512, 1024, 2, 128, -1),
+    (256, 384, 5, 128, 128),
+    (512, 1024, 32, 128, 128),  # prefill kernels: two launches
+]
+
+
+@pytest.mark.parametrize("hidden,inter,batch,gg,dg", CASES)
+def test_fused_mlp_vs_two_launches_and_oracle(dev, hidden, inter, batch, gg, dg):
+    from neurova_amd import capi
+
+    print_case("mlp_fused", hidden, inter, batch, gg, dg,
+               "launches", capi.marlin_mlp_fused_launches(batch, hidden, inter, gg, dg, capi.MLP_ONE_LAUNCH))
+    gu_q, gu_s, d_q, d_s, x = _problem(hidden, inter, batch, gg, dg, seed=batch + hidden)
+    args = [to_dev(a, dev) for a in (x, gu_q, gu_s, d_q, d_s)]
+    got = _fused(dev, *args, hidden, inter, gg, dg, mode=capi.MLP_ONE_LAUNCH)
+    ref, mixed = _two_launches(dev, *args, hidden, inter, gg, dg)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)), "fused != gate_up + silu-gated down"
+    for mode in (capi.MLP_AUTO, capi.MLP_TWO_LAUNCHES):
+        again = _fused(dev, *args, hidden, inter, gg, dg, mode=mode)
+        assert np.array_equal(again.view(np.uint16), ref.view(np.uint16)), mode
+    # oracle: the gate_up projection, then the SiLU-gated down over the GPU's own [g | u]
+    assert_close_f16(mixed, O.marlin_gemm(x, gu_q, gu_s, gg), what="gate_up")
+    assert_close_f16(got, O.marlin_gemm_silu_packed(mixed, d_q, d_s, inter, dg), what="down(silu)")
+
+
+@pytest.mark.parametrize("batch", [1, 4, 16])
+def test_fused_mlp_model_shape_one_launch(dev, batch):
+    from neurova_amd import capi
+
+    launches = capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128, capi.MLP_ONE_LAUNCH)
+    print_case("mlp_fused_model", batch, "launches", launches)
+    assert launches == 1
+    # auto: the two launches at batch 1, one launch from batch 2 on
+    assert capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128) == (2 if batch == 1 else 1)
+    args = _problem_dev(HIDDEN, INTER, batch, 7 + batch, dev)
+    got = _fused(dev, *args, HIDDEN, INTER, 128, 128)
+    ref, _ = _two_launches(dev, *args, HIDDEN, INTER, 128, 128)
+    assert np.array_equal(got.view(np.uint16), ref.view(np.uint16))
+
+
+def test_fused_mlp_back_to_back_calls_share_workspace(dev):
+    """Two calls on one workspace, the second with a smaller batch: each as the
+    two launches give, and the workspace zero after each."""
+    import torch
+    from neurova_amd import capi
+
+    print_case("mlp_fused_b2b", HIDDEN, INTER)
+    n_ws = max(capi.marlin_mlp_fused_workspace_len(b, HIDDEN, INTER) for b in (16, 1))
+    ws = torch.zeros((n_ws,), dtype=torch.int32, device=dev)
+    for batch in (16, 1):
+        args = _problem_dev(HIDDEN, INTER, batch, 100 + batch, dev)
+        got = _fused(dev, *args, HIDDEN, INTER, 128, 128, ws=ws)
+        ref, _ = _two_launches(dev, *args, HIDDEN, INTER, 128, 128)
+        assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)), batch
