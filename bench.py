@@ -325,6 +325,51 @@ def gemm_probe(torch, lc, dev, calls=6):
     log(f"[gemm-probe] {calls} calls of each M=2048 shape")
 
 
+def mlp_probe(torch, dev, calls=40):
+    """The production MLP at the model's shape (hidden 5120, intermediate
+    17408, W4 g128) for M = 1, 4, 16: `calls` graph-replayed calls of the two
+    projections and of the one-launch kernel (lb_marlin_mlp_fused, mode 1),
+    over 4 rotating weight sets, for the kernel-trace runs."""
+    from neurova_amd import capi
+
+    h, it, sets = DecodeStep.HIDDEN, DecodeStep.INTER, 4
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(5)
+
+    def tensor(k, n):
+        q = torch.randint(-2 ** 31, 2 ** 31, (k // 16, 2 * n), dtype=torch.int32, device=dev, generator=gen)
+        s = (torch.randn((k // 128, n), device=dev, generator=gen) * 0.01).abs_().add_(1e-3).half()
+        return q, s
+
+    w = [(tensor(h, 2 * it), tensor(it, h)) for _ in range(sets)]
+    for m in (1, 4, 16):
+        x = torch.randn((m, h), device=dev, generator=gen).half()
+        mixed = torch.empty((m, 2 * it), dtype=torch.float16, device=dev)
+        out = torch.empty((m, h), dtype=torch.float16, device=dev)
+        ws = torch.zeros((max(2 * it // 128 * 16, capi.marlin_mlp_fused_workspace_len(m, h, it)),), dtype=torch.int32,
+                         device=dev)
+        sc1 = torch.empty((capi.marlin_scratch_bytes(m, 2 * it, h, 128),), dtype=torch.uint8, device=dev)
+        sc2 = torch.empty((capi.marlin_scratch_bytes(m, h, it, 128),), dtype=torch.uint8, device=dev)
+        fsc = torch.empty((capi.marlin_mlp_fused_scratch_bytes(m, h, it),), dtype=torch.uint8, device=dev)
+
+        def pair(i):
+            (gq, gs), (dq, ds) = w[i % sets]
+            assert capi.marlin_gemm(x, gq, mixed, gs, ws, 128, sc1) == 0
+            assert capi.marlin_gemm_silu_packed(mixed, dq, out, ds, ws, 128, sc2) == 0
+
+        def fused(i):
+            (gq, gs), (dq, ds) = w[i % sets]
+            assert capi.marlin_mlp_fused(x, gq, gs, dq, ds, out, h, it, 128, 128, ws, fsc,
+                                         mode=capi.MLP_ONE_LAUNCH) == 0
+
+        for name, fn in (("two launches", pair), ("one launch", fused)):
+            ms, st = time_calls(torch, fn, sets, calls, sets, True)
+            log(f"[mlp-probe] M={m:2d} {name}: {ms * 1e3 / st:.2f} us per MLP")
+        assert int(ws.abs().sum()) == 0
+    del w
+    torch.cuda.empty_cache()
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -336,6 +381,7 @@ def main():
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true", help="run the counter-calibration probe and exit")
     ap.add_argument("--gemm-probe", action="store_true", help="run the prefill GEMM counter probe and exit")
+    ap.add_argument("--mlp-probe", action="store_true", help="time the decode MLP (two launches / one launch) and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -357,6 +403,9 @@ def main():
         return
     if args.gemm_probe:
         gemm_probe(torch, lc, dev)
+        return
+    if args.mlp_probe:
+        mlp_probe(torch, dev)
         return
     use_graph = not args.no_graph
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; graph={use_graph}")
