@@ -32,6 +32,7 @@ struct Params {
   int64_t rows, packed_cols, scale_cols;
   int64_t cols, group;
   int batch;
+  int unit_shift;        // LDS kernel: log2(group / 32)
 };
 
 // Code t (0..31) of a 32-code unit held in BITS dwords w[].
@@ -169,6 +170,229 @@ __global__ __launch_bounds__(kThreads) void rowwise_fast_kernel(Params p) {
     }
 }
 
+// ---------------------------------------------------------------------------
+// Single-row GEMV with the activation row staged in LDS (batch 1, 2/3/4/8 bits,
+// columns a multiple of 32).
+//
+// A 32-code unit (BITS dwords) is decoded into 16 fp16 pairs with one AND per
+// pair: two codes that sit at the same bit offset `off` of the two 16-bit
+// halves of a word (after at most one shift, bit-field insert, align or byte
+// permute) are kept as they lie, which read as the fp16 subnormals
+// (c * 2^off * 2^-24, c' * 2^off * 2^-24), exact.  The workgroup stages the
+// activation row once, permuted into the same pair order, so v_dot2_f32_f16
+// of a code pair and its activation pair adds the exact x * c * 2^(off-24)
+// per code; pairs of one offset share an fp32 accumulator, and the unit's
+// sum(x * c) is those sums times 2^(24-off) (exact).  The zero point's share
+// z * sum(x) is staged per unit beside the activations and subtracted once,
+// and the group scale multiplies the unit sum once, as in the fast path.
+// (Scaling the activations by 2^-off instead would flush small ones: fp16
+// arithmetic results below 2^-14 are flushed to zero here.)  Each wave
+// computes R rows (of NW matrices) from one LDS read of the activations.
+// ---------------------------------------------------------------------------
+#ifndef LB_RW_LDS_WAVES
+#define LB_RW_LDS_WAVES 4
+#endif
+#ifndef LB_RW_LDS_ROWS
+#define LB_RW_LDS_ROWS 2
+#endif
+constexpr int kLdsWaves = LB_RW_LDS_WAVES;         // waves (rows x R) per workgroup
+constexpr int kLdsRows = LB_RW_LDS_ROWS;           // rows per wave (one matrix)
+constexpr int kLdsThreads = kLdsWaves * kWave;
+constexpr int kLdsUnitBytes = 68;                  // 16 staged pair words + the unit's zero-point share
+constexpr int64_t kLdsMaxBytes = 64 * 1024;
+
+// Pair q (0..15) of a 32-code unit: codes (lo, hi) and their bit offset.  The
+// decode below produces the pairs in this order.
+__host__ __device__ constexpr int pair_lo(int bits, int q) {
+  return bits == 2 ? 16 * (q >> 3) + (q & 7)
+       : bits == 3 ? (q < 5 ? q : q < 9 ? q + 1 : q < 14 ? q + 2 : (q == 14 ? 5 : 10))
+       : bits == 4 ? 8 * (q >> 2) + (q & 3)
+       : 4 * (q >> 1) + (q & 1);
+}
+__host__ __device__ constexpr int pair_hi(int bits, int q) {
+  return bits == 2 ? pair_lo(2, q) + 8 : bits == 3 ? pair_lo(3, q) + 16 : bits == 4 ? pair_lo(4, q) + 4 : pair_lo(8, q) + 2;
+}
+// Offset classes: b2 {0,2,4,6,8}, b3 {0..7}, b4 {0,4}, b8 {0}.
+__host__ __device__ constexpr int n_classes(int bits) { return bits == 2 ? 5 : bits == 3 ? 8 : bits == 4 ? 2 : 1; }
+__host__ __device__ constexpr int class_of_off(int bits, int off) { return bits == 2 ? off / 2 : bits == 4 ? off / 4 : off; }
+__host__ __device__ constexpr int off_of_class(int bits, int c) { return bits == 2 ? 2 * c : bits == 4 ? 4 * c : c; }
+__host__ __device__ constexpr int pair_off(int bits, int q) {
+  return bits == 2 ? ((q & 7) < 5 ? 2 * (q & 7) : 2 * (q & 7) - 6)
+       : bits == 3 ? (q == 0 ? 0 : q == 1 ? 3 : q == 2 ? 6 : q == 3 ? 3 : q == 4 ? 6 : q == 5 ? 2 : q == 6 ? 5
+                      : q == 7 ? 2 : q == 8 ? 5 : q == 9 ? 1 : q == 10 ? 4 : q == 11 ? 7 : q == 12 ? 4
+                      : q == 13 ? 7 : 0)
+       : bits == 4 ? 4 * (q & 1)
+       : 0;
+}
+
+template <int BITS>
+__device__ __forceinline__ void decode_unit(const uint32_t* w, uint32_t (&b)[16]) {
+  if constexpr (BITS == 2) {
+#pragma unroll
+    for (int d = 0; d < 2; ++d) {
+      const uint32_t x = w[d], xs = x >> 6;
+      b[8 * d + 0] = x & 0x00030003u;
+      b[8 * d + 1] = x & 0x000C000Cu;
+      b[8 * d + 2] = x & 0x00300030u;
+      b[8 * d + 3] = x & 0x00C000C0u;
+      b[8 * d + 4] = x & 0x03000300u;
+      b[8 * d + 5] = xs & 0x00300030u;
+      b[8 * d + 6] = xs & 0x00C000C0u;
+      b[8 * d + 7] = xs & 0x03000300u;
+    }
+  } else if constexpr (BITS == 3) {
+    // unit bits [0,16) | [48,64), [16,32) | [64,80), [32,48) | [80,96), and
+    // the four codes that straddle those ranges (5, 10, 21, 26)
+    const uint32_t m0 = (w[0] & 0x0000ffffu) | (w[1] & 0xffff0000u), m0s = m0 >> 6;
+    const uint32_t m1 = __builtin_amdgcn_alignbit(w[2], w[0], 16), m1s = m1 >> 6;
+    const uint32_t m2 = (w[1] & 0x0000ffffu) | (w[2] & 0xffff0000u), m2s = m2 >> 6;
+    b[0] = m0 & 0x00070007u;
+    b[1] = m0 & 0x00380038u;
+    b[2] = m0 & 0x01c001c0u;
+    b[3] = m0s & 0x00380038u;
+    b[4] = m0s & 0x01c001c0u;
+    b[5] = m1 & 0x001c001cu;
+    b[6] = m1 & 0x00e000e0u;
+    b[7] = m1s & 0x001c001cu;
+    b[8] = m1s & 0x00e000e0u;
+    b[9] = m2 & 0x000e000eu;
+    b[10] = m2 & 0x00700070u;
+    b[11] = m2 & 0x03800380u;
+    b[12] = m2s & 0x00700070u;
+    b[13] = m2s & 0x03800380u;
+    const uint32_t d0 = __builtin_amdgcn_perm(__builtin_amdgcn_alignbit(w[2], w[1], 31), w[0] >> 15, 0x05040100u);
+    const uint32_t d1 = __builtin_amdgcn_perm(w[2] >> 14, __builtin_amdgcn_alignbit(w[1], w[0], 30), 0x05040100u);
+    b[14] = d0 & 0x00070007u;
+    b[15] = d1 & 0x00070007u;
+  } else if constexpr (BITS == 4) {
+#pragma unroll
+    for (int d = 0; d < 4; ++d) {
+      const uint32_t x = w[d], xs = x >> 8;
+      b[4 * d + 0] = x & 0x000f000fu;
+      b[4 * d + 1] = x & 0x00f000f0u;
+      b[4 * d + 2] = xs & 0x000f000fu;
+      b[4 * d + 3] = xs & 0x00f000f0u;
+    }
+  } else {
+    static_assert(BITS == 8, "2, 3, 4 or 8 bits");
+#pragma unroll
+    for (int d = 0; d < 8; ++d) {
+      b[2 * d + 0] = w[d] & 0x00ff00ffu;
+      b[2 * d + 1] = (w[d] >> 8) & 0x00ff00ffu;
+    }
+  }
+}
+
+template <int BITS, int NW, int R>
+__global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(Params p) {
+  extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  const int units = (int)(p.cols >> 5);
+  u32x4* xt = reinterpret_cast<u32x4*>(smem);                           // [4][units] pair words
+  float* corr = reinterpret_cast<float*>(smem + (size_t)units * 64);    // [units]
+  const int tid = threadIdx.x;
+  constexpr int z = 1 << (BITS - 1);
+
+  // ---- stage the activation row in pair order, and each unit's z * sum(x) ----
+  for (int u = tid; u < units; u += kLdsThreads) {
+    const uint4* xs = reinterpret_cast<const uint4*>(p.x + (int64_t)u * 32);
+    uint32_t xd[16];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const uint4 t4 = xs[v];
+      xd[4 * v] = t4.x;
+      xd[4 * v + 1] = t4.y;
+      xd[4 * v + 2] = t4.z;
+      xd[4 * v + 3] = t4.w;
+    }
+    uint32_t pw[16];
+    float sx = 0.f;  // sum of the unit's activations
+#pragma unroll
+    for (int q = 0; q < 16; ++q) {
+      const int lo = pair_lo(BITS, q), hi = pair_hi(BITS, q);
+      const uint32_t sel = (uint32_t)(2 * (lo & 1)) | ((uint32_t)(2 * (lo & 1) + 1) << 8) |
+                           ((uint32_t)(4 + 2 * (hi & 1)) << 16) | ((uint32_t)(5 + 2 * (hi & 1)) << 24);
+      const uint32_t v = __builtin_amdgcn_perm(xd[hi >> 1], xd[lo >> 1], sel);
+      pw[q] = v;
+      sx = __builtin_amdgcn_fdot2(as_h2(v), (f16x2){(f16)1.0f, (f16)1.0f}, sx, false);
+    }
+#pragma unroll
+    for (int v = 0; v < 4; ++v) xt[v * units + u] = (u32x4){pw[4 * v], pw[4 * v + 1], pw[4 * v + 2], pw[4 * v + 3]};
+    corr[u] = (float)z * sx;
+  }
+  __syncthreads();
+
+  // ---- R rows of each of NW matrices per wave ----
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+  const int64_t row0 = ((int64_t)blockIdx.x * kLdsWaves + wave) * R;
+  // per-row bases, wave-uniform; 32-bit offsets from them in the loop
+  const uint32_t* qrow[NW][R];
+  const uint16_t* srow[NW][R];
+#pragma unroll
+  for (int a = 0; a < NW; ++a)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = row0 + r < p.rows ? row0 + r : p.rows - 1;
+      qrow[a][r] = reinterpret_cast<const uint32_t*>(p.q[a] + row * p.packed_cols);
+      srow[a][r] = p.s[a] + row * p.scale_cols;
+    }
+  float acc[NW][R];
+#pragma unroll
+  for (int a = 0; a < NW; ++a)
+#pragma unroll
+    for (int r = 0; r < R; ++r) acc[a][r] = 0.f;
+  for (int u = lane; u < units; u += kWave) {
+    const uint32_t grp = (uint32_t)u >> p.unit_shift;
+    uint32_t w[NW][R][BITS];
+    float sc[NW][R];
+#pragma unroll
+    for (int a = 0; a < NW; ++a)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t* src = qrow[a][r] + (uint32_t)u * BITS;
+#pragma unroll
+        for (int d = 0; d < BITS; ++d) w[a][r][d] = __builtin_nontemporal_load(src + d);
+        sc[a][r] = h2f(srow[a][r][grp]);
+      }
+    uint32_t xq[16];
+#pragma unroll
+    for (int v = 0; v < 4; ++v) {
+      const u32x4 t4 = xt[v * units + u];
+      xq[4 * v] = t4[0];
+      xq[4 * v + 1] = t4[1];
+      xq[4 * v + 2] = t4[2];
+      xq[4 * v + 3] = t4[3];
+    }
+    const float cu = corr[u];
+#pragma unroll
+    for (int a = 0; a < NW; ++a)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        uint32_t b[16];
+        decode_unit<BITS>(w[a][r], b);
+        constexpr int NC = n_classes(BITS);
+        float tc[NC];
+#pragma unroll
+        for (int c = 0; c < NC; ++c) tc[c] = 0.f;
+#pragma unroll
+        for (int q = 0; q < 16; ++q) {
+          const int c = class_of_off(BITS, pair_off(BITS, q));
+          tc[c] = __builtin_amdgcn_fdot2(as_h2(b[q]), as_h2(xq[q]), tc[c], false);
+        }
+        float t = -cu;
+#pragma unroll
+        for (int c = 0; c < NC; ++c) t = __builtin_fmaf(tc[c], (float)(1 << (24 - off_of_class(BITS, c))), t);
+        acc[a][r] += t * sc[a][r];
+      }
+  }
+#pragma unroll
+  for (int a = 0; a < NW; ++a)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const float v = wave_sum(acc[a][r]);
+      if (lane == 0 && row0 + r < p.rows) p.y[a][row0 + r] = f2h(v);
+    }
+}
+
 // Any stride / group size: bytes as in the reference's qb_lowbit_value.
 template <int NW, int BT>
 __global__ __launch_bounds__(kThreads) void rowwise_general_kernel(Params p, int bits) {
@@ -247,9 +471,34 @@ int launch_bt(const Params& p, int bits, bool fast, hipStream_t st) {
   return lbh::launch_status();
 }
 
+template <int NW, int R>
+int launch_lds(const Params& p, int bits, hipStream_t st) {
+  const int64_t rows_per_wg = (int64_t)kLdsWaves * R;
+  dim3 grid((unsigned)((p.rows + rows_per_wg - 1) / rows_per_wg));
+  const size_t lds = (size_t)(p.cols >> 5) * kLdsUnitBytes;
+  switch (bits) {
+#define LB_LCASE(B) \
+  case B: hipLaunchKernelGGL((rowwise_lds_kernel<B, NW, R>), grid, dim3(kLdsThreads), lds, st, p); break;
+    LB_LCASE(2) LB_LCASE(3) LB_LCASE(4) LB_LCASE(8)
+#undef LB_LCASE
+    default: return LB_ERR_ARG;
+  }
+  return lbh::launch_status();
+}
+
 int launch(Params p, int nw, int bits, hipStream_t st) {
   const bool fast = (p.packed_cols % 4 == 0) && lbh::aligned(p.q[0], 4) && (nw == 1 || lbh::aligned(p.q[1], 4)) &&
                     (p.group % 32 == 0) && (p.x_stride % 8 == 0) && lbh::aligned(p.x, 16);
+  // one activation row, whole units, staged in LDS
+  const int64_t gu = p.group / 32;  // units per group
+  const bool lds = fast && p.batch == 1 && p.cols % 32 == 0 && (bits == 2 || bits == 3 || bits == 4 || bits == 8) &&
+                   (p.cols >> 5) * kLdsUnitBytes <= kLdsMaxBytes && (gu & (gu - 1)) == 0 &&
+                   p.packed_cols * (p.rows > 0 ? 1 : 0) <= (int64_t)0xffffffff / 2;
+  if (lds) {
+    p.unit_shift = 0;
+    while ((int64_t(1) << p.unit_shift) < gu) ++p.unit_shift;
+  }
+  if (lds) return nw == 1 ? launch_lds<1, kLdsRows>(p, bits, st) : launch_lds<2, kLdsRows / 2>(p, bits, st);
   if (p.batch <= 1) {
     return nw == 1 ? launch_bt<1, 1>(p, bits, fast, st) : launch_bt<2, 1>(p, bits, fast, st);
   }

@@ -129,7 +129,12 @@ def test_gemm_equals_repeated_gemv(dev, bits, cols, batch):
     y = lc.lowbit_gemm(q, s, xd, cols, 128, bits)
     rep = torch.stack([lc.lowbit_gemv(q, s, xd[i], cols, 128, bits) for i in range(batch)])
     torch.cuda.synchronize()
-    assert torch.equal(y, rep)
+    if batch == 1 or cols % 32:
+        assert torch.equal(y, rep)  # the same kernel
+    else:
+        # a single row of whole 32-code units takes the LDS-staged kernel, whose
+        # fp32 sums are ordered differently: both within the parity bar
+        assert_close_f16(to_np(rep), O.rowwise_gemm(packed, scales, x, cols, 128, bits), what="repeated gemv")
     assert_close_f16(to_np(y), O.rowwise_gemm(packed, scales, x, cols, 128, bits))
 
 
