@@ -190,10 +190,10 @@ __global__ __launch_bounds__(kThreads) void rowwise_fast_kernel(Params p) {
 // computes R rows (of NW matrices) from one LDS read of the activations.
 // ---------------------------------------------------------------------------
 #ifndef LB_RW_LDS_WAVES
-#define LB_RW_LDS_WAVES 4
+#define LB_RW_LDS_WAVES 8
 #endif
 #ifndef LB_RW_LDS_ROWS
-#define LB_RW_LDS_ROWS 2
+#define LB_RW_LDS_ROWS 1
 #endif
 constexpr int kLdsWaves = LB_RW_LDS_WAVES;         // waves (rows x R) per workgroup
 constexpr int kLdsRows = LB_RW_LDS_ROWS;           // rows per wave (one matrix)
@@ -381,7 +381,7 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(Params p) {
         float t = -cu;
 #pragma unroll
         for (int c = 0; c < NC; ++c) t = __builtin_fmaf(tc[c], (float)(1 << (24 - off_of_class(BITS, c))), t);
-        acc[a][r] += t * sc[a][r];
+        acc[a][r] = __builtin_fmaf(t, sc[a][r], acc[a][r]);  // explicit: one rounding in every instantiation
       }
   }
 #pragma unroll
@@ -498,7 +498,7 @@ int launch(Params p, int nw, int bits, hipStream_t st) {
     p.unit_shift = 0;
     while ((int64_t(1) << p.unit_shift) < gu) ++p.unit_shift;
   }
-  if (lds) return nw == 1 ? launch_lds<1, kLdsRows>(p, bits, st) : launch_lds<2, kLdsRows / 2>(p, bits, st);
+  if (lds) return nw == 1 ? launch_lds<1, kLdsRows>(p, bits, st) : launch_lds<2, (kLdsRows + 1) / 2>(p, bits, st);
   if (p.batch <= 1) {
     return nw == 1 ? launch_bt<1, 1>(p, bits, fast, st) : launch_bt<2, 1>(p, bits, fast, st);
   }

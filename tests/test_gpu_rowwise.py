@@ -101,6 +101,27 @@ def test_pair_padded_equals_two_singles(dev, bits):
     assert_close_f16(to_np(pb_out), O.rowwise_gemv(pb, sb, x[0], cols, 64, bits))
 
 
+@pytest.mark.parametrize("bits", [2, 3, 4, 8])
+@pytest.mark.parametrize("rows,cols,group", [(41, 2048, 128), (7, 5120, 64), (96, 1024, 32)])
+def test_pair_whole_units_equals_two_singles(dev, bits, rows, cols, group):
+    """Whole 32-code units and one activation row: the pair takes the LDS-staged
+    kernel with both matrices per wave; each output equals its single GEMV."""
+    import torch
+    import langburst_cuda as lc
+
+    print_case("pair-units", bits, rows, cols, group)
+    _, pa, sa, x = O.make_rowwise_inputs(rows, cols, bits, group, seed=270 + bits + rows)
+    _, pb, sb, _ = O.make_rowwise_inputs(rows, cols, bits, group, seed=280 + bits + rows)
+    qa, qb, sca, scb, xd = (to_dev(a, dev) for a in (pa, pb, sa, sb, x[0]))
+    ya = lc.lowbit_gemv(qa, sca, xd, cols, group, bits)
+    yb = lc.lowbit_gemv(qb, scb, xd, cols, group, bits)
+    pa_out, pb_out = lc.lowbit_gemv_pair(qa, sca, qb, scb, xd, cols, group, bits)
+    torch.cuda.synchronize()
+    assert torch.equal(pa_out, ya) and torch.equal(pb_out, yb)
+    assert_close_f16(to_np(pa_out), O.rowwise_gemv(pa, sa, x[0], cols, group, bits), what="pair a")
+    assert_close_f16(to_np(pb_out), O.rowwise_gemv(pb, sb, x[0], cols, group, bits), what="pair b")
+
+
 @pytest.mark.parametrize("bits", [3, 4])
 def test_pair_equals_two_singles(dev, bits):
     import torch
