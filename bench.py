@@ -362,8 +362,17 @@ def mlp_probe(torch, dev, calls=40):
             assert capi.marlin_mlp_fused(x, gq, gs, dq, ds, out, h, it, 128, 128, ws, fsc,
                                          mode=capi.MLP_ONE_LAUNCH) == 0
 
-        for name, fn in (("two launches", pair), ("one launch", fused)):
-            ms, st = time_calls(torch, fn, sets, calls, sets, True)
+        accum = torch.empty((m, h), dtype=torch.float32, device=dev)
+        sync = torch.zeros((2 * m,), dtype=torch.int32, device=dev)
+        ssc = torch.empty((capi.marlin_mlp_scratch_bytes(m, h, it),), dtype=torch.uint8, device=dev)
+
+        def streaming(i):
+            (gq, gs), (dq, ds) = w[i % sets]
+            assert capi.marlin_mlp_streaming(gq, gs, dq, ds, x, out, accum, sync, h, it, 128, 128, ssc) == 0
+
+        for name, fn, n_calls in (("two launches", pair, calls), ("one launch", fused, calls),
+                                  ("streaming (fp32 numerics)", streaming, sets)):
+            ms, st = time_calls(torch, fn, sets, n_calls, sets, True)
             log(f"[mlp-probe] M={m:2d} {name}: {ms * 1e3 / st:.2f} us per MLP")
         assert int(ws.abs().sum()) == 0
     del w
