@@ -308,6 +308,58 @@ void lowbit_marlin_mlp_streaming_out(torch::Tensor gate_up_qweight, torch::Tenso
   TORCH_CHECK(err == 0, "Marlin streaming MLP failed with code ", err, " (", lb_status_string(err), ")");
 }
 
+// The decode MLP the reference's _fused_marlin_down runs as two ops
+// (langburst/adapters/qwen36_impl/model.py:1460-1470: gate/up GEMM, then the
+// SiLU-packed down GEMM), as one call: one kernel launch for batch 2..16 in
+// mode 0, the same two launches otherwise.  The result is bit-identical to the
+// two ops.  `workspace` is int32, zero on entry, and left zero, except that
+// entry 1 stays 1 if the in-kernel hand-off gave up waiting: the output of that
+// call is then not valid.  Nothing here synchronises, so a caller that wants
+// the check reads entry 1 after the stream has finished.
+void lowbit_marlin_mlp_fused_out(torch::Tensor gate_up_qweight, torch::Tensor gate_up_scales,
+                                 torch::Tensor down_qweight, torch::Tensor down_scales, torch::Tensor x,
+                                 torch::Tensor out, torch::Tensor workspace, int64_t hidden, int64_t intermediate,
+                                 int64_t gate_group_size, int64_t down_group_size, int64_t mode) {
+  LB_CHECK_DEV(gate_up_qweight); LB_CHECK_DEV(gate_up_scales); LB_CHECK_DEV(down_qweight); LB_CHECK_DEV(down_scales);
+  LB_CHECK_DEV(x); LB_CHECK_DEV(out); LB_CHECK_DEV(workspace);
+  LB_CHECK_CONTIG(gate_up_qweight); LB_CHECK_CONTIG(gate_up_scales); LB_CHECK_CONTIG(down_qweight);
+  LB_CHECK_CONTIG(down_scales); LB_CHECK_CONTIG(x); LB_CHECK_CONTIG(out); LB_CHECK_CONTIG(workspace);
+  TORCH_CHECK(gate_up_qweight.scalar_type() == at::kInt && down_qweight.scalar_type() == at::kInt,
+              "Marlin qweight must be int32");
+  LB_CHECK_HALF(gate_up_scales); LB_CHECK_HALF(down_scales); LB_CHECK_HALF(x); LB_CHECK_HALF(out);
+  TORCH_CHECK(workspace.scalar_type() == at::kInt, "workspace must be int32");
+  TORCH_CHECK(x.dim() == 2, "x must be [batch, hidden]");
+  const int64_t batch = x.size(0);
+  TORCH_CHECK(x.size(1) == hidden, "x hidden mismatch");
+  TORCH_CHECK(out.dim() == 2 && out.size(0) == batch && out.size(1) == hidden, "out must be [batch, hidden]");
+  TORCH_CHECK(gate_up_qweight.dim() == 2 && gate_up_qweight.size(0) == hidden / 16 &&
+                  gate_up_qweight.size(1) == 4 * intermediate,
+              "gate_up qweight must be [hidden/16, (2*intermediate)*2]");
+  TORCH_CHECK(down_qweight.dim() == 2 && down_qweight.size(0) == intermediate / 16 &&
+                  down_qweight.size(1) == 2 * hidden,
+              "down qweight must be [intermediate/16, hidden*2]");
+  int64_t gate_group = gate_group_size, down_group = down_group_size;
+  if (gate_group <= 0 || gate_group == hidden) gate_group = -1;
+  if (down_group <= 0 || down_group == intermediate) down_group = -1;
+  const int64_t gate_groups = gate_group == 128 ? hidden / 128 : 1;
+  const int64_t down_groups = down_group == 128 ? intermediate / 128 : 1;
+  TORCH_CHECK(gate_up_scales.dim() == 2 && gate_up_scales.size(0) == gate_groups &&
+                  gate_up_scales.size(1) == 2 * intermediate,
+              "gate_up scales shape mismatch");
+  TORCH_CHECK(down_scales.dim() == 2 && down_scales.size(0) == down_groups && down_scales.size(1) == hidden,
+              "down scales shape mismatch");
+  const int64_t ws_need = lb_marlin_mlp_fused_workspace_len(batch, hidden, intermediate);
+  TORCH_CHECK(workspace.numel() >= ws_need, "workspace must hold at least ", ws_need, " int32 elements");
+  const c10::DeviceGuard guard(x.device());
+  const size_t bytes = lb_marlin_mlp_fused_scratch_bytes(batch, hidden, intermediate);
+  auto scratch = torch::empty({(int64_t)std::max<size_t>(bytes, 1)}, x.options().dtype(torch::kUInt8));
+  lb_ok(lb_marlin_mlp_fused(h16(x), gate_up_qweight.data_ptr<int32_t>(), h16(gate_up_scales),
+                            down_qweight.data_ptr<int32_t>(), h16(down_scales), h16m(out), batch, hidden,
+                            intermediate, gate_group, down_group, (int32_t)mode, workspace.data_ptr<int32_t>(),
+                            workspace.numel(), scratch.data_ptr(), (size_t)scratch.numel(), stream_of(x)),
+        "lowbit_marlin_mlp_fused_out");
+}
+
 // Dense fp16 W[N, K] of a Marlin tensor (no reference op; the reference's
 // inverse reader is csrc/marlin_mlp_stream.cu:109-133).
 torch::Tensor lowbit_marlin_dequant(torch::Tensor qweight, torch::Tensor scales, int64_t cols, int64_t group_size) {
@@ -366,6 +418,17 @@ PYBIND11_MODULE(langburst_cuda, m) {
         py::arg("cols"), py::arg("group_size"));
   m.def("lowbit_marlin_dequant", &lowbit_marlin_dequant, "Dense fp16 W[N, K] of a Marlin tensor",
         py::arg("qweight"), py::arg("scales"), py::arg("cols"), py::arg("group_size"));
+  m.def("lowbit_marlin_mlp_fused_out", &lowbit_marlin_mlp_fused_out,
+        "Marlin W4A16 decode MLP: down(SiLU(gate) * up) of x, one launch for batch 2..16 in mode 0",
+        py::arg("gate_up_qweight"), py::arg("gate_up_scales"), py::arg("down_qweight"), py::arg("down_scales"),
+        py::arg("x"), py::arg("out"), py::arg("workspace"), py::arg("hidden"), py::arg("intermediate"),
+        py::arg("gate_group_size"), py::arg("down_group_size"), py::arg("mode") = 0);
+  m.def("lowbit_marlin_mlp_fused_workspace_len",
+        [](int64_t batch, int64_t hidden, int64_t intermediate) {
+          return lb_marlin_mlp_fused_workspace_len(batch, hidden, intermediate);
+        },
+        "int32 elements of the workspace lowbit_marlin_mlp_fused_out needs", py::arg("batch"), py::arg("hidden"),
+        py::arg("intermediate"));
   m.def("abi_version", []() { return lb_abi_version(); });
   m.attr("__provides__") = py::make_tuple("lowbit_gemv", "lowbit_row_dequant", "lowbit_gemv_pair", "lowbit_gemm",
                                           "lowbit_marlin_gemm", "lowbit_marlin_gemm_out",

@@ -179,6 +179,13 @@ def test_module_surface_and_host_tensor_messages(built):
     xm = torch.zeros((1, 256), dtype=torch.float16)
     with pytest.raises(RuntimeError, match="must be CUDA"):
         lc.lowbit_marlin_gemm(qm, sm, xm, 256, 128)
+    # the one-call decode MLP (no reference op of its own) checks like the streaming op
+    assert lc.lowbit_marlin_mlp_fused_workspace_len(1, 5120, 17408) == capi.lib().lb_marlin_mlp_fused_workspace_len(
+        1, 5120, 17408)
+    gu = torch.zeros((16, 4 * 512), dtype=torch.int32)
+    with pytest.raises(RuntimeError, match="must be CUDA"):
+        lc.lowbit_marlin_mlp_fused_out(gu, sm, qm, sm, xm, xm, torch.zeros(8, dtype=torch.int32), 256, 512, 128,
+                                       128)
 
 
 def test_ops_never_fall_back_to_cpu(monkeypatch, built):

@@ -144,3 +144,35 @@ def test_fused_mlp_back_to_back_calls_share_workspace(dev):
         got = _fused(dev, *args, HIDDEN, INTER, 128, 128, ws=ws)
         ref, _ = _two_launches(dev, *args, HIDDEN, INTER, 128, 128)
         assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)), batch
+
+
+@pytest.mark.parametrize("batch", [1, 4])
+def test_torch_op_matches_reference_op_sequence(dev, batch):
+    """``langburst_cuda.lowbit_marlin_mlp_fused_out`` against the two ops the
+    reference's ``_fused_marlin_down`` calls (``lowbit_marlin_gemm_out``, then
+    ``lowbit_marlin_gemm_silu_packed_out`` with the reference's workspace size,
+    ``loader.py:337-368``): bit-equal to the C-ABI two launches, within the
+    parity bar of the reference op sequence, workspace left zero."""
+    import torch
+    import langburst_cuda as lc
+
+    print_case("mlp_fused_op", batch)
+    x, gu_q, gu_s, d_q, d_s = _problem_dev(HIDDEN, INTER, batch, 50 + batch, dev)
+    ws = torch.zeros((lc.lowbit_marlin_mlp_fused_workspace_len(batch, HIDDEN, INTER),), dtype=torch.int32,
+                     device=dev)
+    out = torch.empty((batch, HIDDEN), dtype=torch.float16, device=dev)
+    lc.lowbit_marlin_mlp_fused_out(gu_q, gu_s, d_q, d_s, x, out, ws, HIDDEN, INTER, 128, 128)
+    mixed = torch.empty((batch, 2 * INTER), dtype=torch.float16, device=dev)
+    ws_gu = torch.zeros((2 * INTER // 128 * 16,), dtype=torch.int32, device=dev)
+    lc.lowbit_marlin_gemm_out(gu_q, gu_s, x, mixed, ws_gu, HIDDEN, 128)
+    ws_d = torch.zeros((HIDDEN // 128 * 16,), dtype=torch.int32, device=dev)
+    ref_out = torch.empty((batch, HIDDEN), dtype=torch.float16, device=dev)
+    lc.lowbit_marlin_gemm_silu_packed_out(d_q, d_s, mixed, ref_out, ws_d, INTER, 128)
+    torch.cuda.synchronize()
+    assert int(ws.abs().sum()) == 0
+    got = to_np(out)
+    two, _ = _two_launches(dev, x, gu_q, gu_s, d_q, d_s, HIDDEN, INTER, 128, 128)
+    assert np.array_equal(got.view(np.uint16), two.view(np.uint16))
+    assert_close_f16(got, to_np(ref_out), what="op vs reference op sequence")
+    with pytest.raises(RuntimeError, match="workspace must hold"):
+        lc.lowbit_marlin_mlp_fused_out(gu_q, gu_s, d_q, d_s, x, out, ws[:8], HIDDEN, INTER, 128, 128)
