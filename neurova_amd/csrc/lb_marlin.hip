@@ -247,8 +247,13 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
   // needs more than kSkinnyMaxSplits k splits to fill the chip: then 2 or 1
   // chunks, whose waves share the workgroup's k range.
   int cpw = 0, s = 0;
+#ifdef LB_SKINNY_CPW
+  constexpr int kCpwWidest = LB_SKINNY_CPW, kCpwNarrowest = LB_SKINNY_CPW;  // schedule sweeps only
+#else
+  constexpr int kCpwWidest = 4, kCpwNarrowest = 1;
+#endif
   if (m <= skinny::kMaxM) {
-    for (int c = 4; c >= 1; c /= 2) {
+    for (int c = kCpwWidest; c >= kCpwNarrowest; c /= 2) {
       const int sc = skinny_splits(m, n, k, workspace_len, c);
       if (sc == 0) continue;
       if (cpw == 0 || sc < s) {
