@@ -169,7 +169,8 @@ int lb_marlin_mlp_streaming(const int32_t* gate_up_qweight, const uint16_t* gate
  *       which a call takes.
  * workspace: int32 [lb_marlin_mlp_fused_workspace_len()], zero on entry, left
  *            zero (entry 1 stays 1 if a hand-off wait gave up: the
- *            output is then not valid).
+ *            output is then not valid, and the workspace must be zeroed
+ *            again before the next call).
  * scratch:   lb_marlin_mlp_fused_scratch_bytes() bytes, 256-byte aligned.
  * Calls that share a workspace must not overlap. */
 size_t lb_marlin_mlp_fused_scratch_bytes(int64_t batch, int64_t hidden, int64_t intermediate);

@@ -314,8 +314,9 @@ void lowbit_marlin_mlp_streaming_out(torch::Tensor gate_up_qweight, torch::Tenso
 // mode 0, the same two launches otherwise.  The result is bit-identical to the
 // two ops.  `workspace` is int32, zero on entry, and left zero, except that
 // entry 1 stays 1 if the in-kernel hand-off gave up waiting: the output of that
-// call is then not valid.  Nothing here synchronises, so a caller that wants
-// the check reads entry 1 after the stream has finished.
+// call is then not valid and the workspace must be zeroed again.  Nothing
+// here synchronises, so a caller that wants the check reads entry 1 after the
+// stream has finished.
 void lowbit_marlin_mlp_fused_out(torch::Tensor gate_up_qweight, torch::Tensor gate_up_scales,
                                  torch::Tensor down_qweight, torch::Tensor down_scales, torch::Tensor x,
                                  torch::Tensor out, torch::Tensor workspace, int64_t hidden, int64_t intermediate,

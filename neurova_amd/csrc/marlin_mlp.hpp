@@ -26,7 +26,9 @@
 // kernel only when the instantiation's occupancy allows it and otherwise runs
 // the two projections.  Each wait is bounded: a workgroup that has polled
 // kSpinLimit times records a fault flag (workspace entry 1) and goes on, so a
-// launch always ends.
+// launch always ends.  After such a fault a late producer may still count a
+// tile once its split's counters were reset, so the caller must zero the
+// workspace again before the next launch.
 
 #pragma once
 #include "marlin_skinny.hpp"
@@ -34,7 +36,7 @@
 namespace lb {
 namespace mlp {
 
-constexpr int kSpinLimit = 1 << 18;  // polls, about 0.1 us apart
+constexpr int kSpinLimit = 1 << 18;  // polls; each waits for its device-scope load, then sleeps 128 cycles
 constexpr int kLineInts = 32;        // one 128-byte line per counter
 constexpr int kMaxSplits = 64;       // down k splits the counters cover
 // workspace layout (int32): [1] fault flag; ready[s] at kReadyBase + kLineInts * s,
