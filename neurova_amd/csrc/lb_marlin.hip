@@ -219,7 +219,9 @@ inline int skinny_splits(int64_t m, int64_t n, int64_t k, int64_t workspace_len,
   const int ksub = skinny::kWaves / cpw;
   const int groups = (int)(k / 128);
   const size_t x_all = (size_t)k * (size_t)m * 2;
-  const bool can_split = workspace_len >= (int64_t)n_cg + 1;
+  // split counters: one per chunk for wide tiles (each wave hands off on its
+  // own), one per tile otherwise
+  const bool can_split = workspace_len >= 1 + (cpw == skinny::kWaves ? n / 64 : (int64_t)n_cg);
   // As many k splits as fit in one wave of resident workgroups: a second,
   // partial wave would cost a whole workgroup's time for a few tiles.
   int s = (kSkinnyWGsPerCU * device_cus()) / n_cg;
@@ -231,6 +233,7 @@ inline int skinny_splits(int64_t m, int64_t n, int64_t k, int64_t workspace_len,
   const int s_lds = (int)((x_all + kSkinnyMaxX - 1) / kSkinnyMaxX);
   if (s < s_lds) s = s_lds;
   if (s > groups / ksub) s = groups / ksub;  // every wave at least one group
+  if (s > 256) s = 256;  // the kernel's split arithmetic is 32-bit: groups * S < 2^32
   if (s < 1) s = 1;
   if (!can_split) s = 1;
   if (groups / s < ksub) return 0;
@@ -323,7 +326,8 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
 // Workspace entries a launch uses: [0] the argmax arrival counter, [1 + t]
 // the split counters (decode: every column tile; GEMM: every tail tile).
 inline int64_t counters_needed(const Plan& pl, bool argmax) {
-  if (pl.skinny && pl.splits > 1) return 1 + (int64_t)pl.n_cg;
+  // plain stores on wide tiles count per 64-column chunk (see skinny::wave_epilogue)
+  if (pl.skinny && pl.splits > 1) return 1 + (int64_t)pl.n_cg * (argmax ? 1 : pl.cpw == skinny::kWaves ? pl.cpw : 1);
   if (!pl.skinny && pl.tail_tiles > 0) return 1 + (int64_t)pl.tail_tiles;
   return argmax ? 1 : 0;
 }
@@ -662,8 +666,10 @@ FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g
   }
   // workspace: the hand-off counters and fault flag, then each projection's counters
   p.ws_up = mlp::kSyncWorkspace;
-  p.ws_down = p.ws_up + 1 + std::max<int64_t>(p.up.n_cg, p.up.tail_tiles);
-  p.ws_len = p.ws_down + 1 + std::max<int64_t>(p.down.n_cg, p.down.tail_tiles);
+  p.ws_down = p.ws_up + std::max<int64_t>(1 + std::max<int64_t>(p.up.n_cg, p.up.tail_tiles),
+                                           marlin::counters_needed(p.up, false));
+  p.ws_len = p.ws_down + std::max<int64_t>(1 + std::max<int64_t>(p.down.n_cg, p.down.tail_tiles),
+                                           marlin::counters_needed(p.down, false));
   return p;
 }
 

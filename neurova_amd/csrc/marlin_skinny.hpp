@@ -116,13 +116,14 @@ __device__ __forceinline__ uint64_t wave_max_u64(uint64_t v) {
   return v;
 }
 
-// Splits are whole scale groups (4 k-steps of 32) balanced over S.
+// Splits are whole scale groups (4 k-steps of 32) balanced over S.  32-bit
+// arithmetic: the host keeps groups * S below 2^32 (K <= 2^30, S <= 256).
 __device__ __forceinline__ void split_range(const Params& p, int split, int& kp0, int& kp1) {
-  const int groups = p.kp_total >> 2;
-  const int g0 = (int)(((int64_t)groups * split) / p.splits);
-  const int g1 = (int)(((int64_t)groups * (split + 1)) / p.splits);
-  kp0 = g0 << 2;
-  kp1 = g1 << 2;
+  const uint32_t groups = (uint32_t)p.kp_total >> 2;
+  const uint32_t g0 = (groups * (uint32_t)split) / (uint32_t)p.splits;
+  const uint32_t g1 = (groups * (uint32_t)(split + 1)) / (uint32_t)p.splits;
+  kp0 = (int)(g0 << 2);
+  kp1 = (int)(g1 << 2);
 }
 
 // Inverse of the per-column scale permutation (quantize.py:66-68).
@@ -149,6 +150,81 @@ __device__ __forceinline__ int tile_chunk(const Params& p, int cg, int c) {
   return cg * CPW + c;
 }
 
+// Plain-store epilogue, one wave on its own (no LDS, no workgroup barrier).
+// The wave holds the fp32 sums of one 64-column chunk over its share of K:
+// acc[j][i] is row 4 (lane >> 4) + i, column 16 j + (lane & 15) of the chunk.
+// Shares are the k splits times the k shares of a workgroup, T = S * ksub,
+// numbered split-major.  T == 1: the wave rounds and stores its outputs.
+// Otherwise it publishes its partial (device-coherent stores into
+// partial [T][M][N]), waits for their acknowledgement, and counts its arrival
+// on the chunk's counter (workspace entry 1 + chunk); the wave that completes
+// the count reads the T partials of the chunk in share order (deterministic),
+// rounds, stores, and resets the counter.  Returns true in the wave that
+// stored the chunk's outputs.
+template <bool GROUPED>
+__device__ __forceinline__ bool wave_epilogue(const Params& p, const f32x4 (&acc)[4], int chunk, int share, int ksub) {
+  const int lane = threadIdx.x & 63;
+  const int mrows = p.m;
+  const int total = p.splits * ksub;
+  const int crow0 = (lane >> 4) * 4;
+  const int col0 = chunk * 64;
+  if (total == 1) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      const int n = col0 + 16 * j + (lane & 15);
+      const f16 cs = GROUPED ? (f16)1.0f : __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const int r = crow0 + i;
+        f16 h = (f16)acc[j][i];
+        if (!GROUPED) h = h * cs;
+        if (r < mrows) p.c[(int64_t)r * p.n + n] = __builtin_bit_cast(uint16_t, h);
+      }
+    }
+    return true;
+  }
+  const int64_t share_stride = (int64_t)mrows * p.n;
+  float* part = p.partial + share * share_stride + col0 + (lane & 15);
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      if (crow0 + i < mrows) publish(part + (int64_t)(crow0 + i) * p.n + 16 * j, acc[j][i]);
+  wait_published();
+  int32_t* ctr = p.counters + 1 + chunk;
+  int prev = 0;
+  if (lane == 0) prev = arrive(ctr);
+  prev = __builtin_amdgcn_readfirstlane(prev);
+  if (prev != total - 1) return false;
+  if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  // lane = column of the chunk; 4 rows x 8 shares of loads in flight
+  const int n = col0 + lane;
+  const float* src = p.partial + n;
+  const f16 cs = GROUPED ? (f16)1.0f : __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
+  for (int r0 = 0; r0 < mrows; r0 += 4) {
+    float sum[4] = {0.f, 0.f, 0.f, 0.f};
+    for (int s0 = 0; s0 < total; s0 += 8) {
+      float t[4][8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int u = 0; u < 8; ++u)
+          t[i][u] = collect(src + (int64_t)min(s0 + u, total - 1) * share_stride + (int64_t)min(r0 + i, mrows - 1) * p.n);
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int u = 0; u < 8; ++u) sum[i] += (s0 + u < total) ? t[i][u] : 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      f16 h = (f16)sum[i];
+      if (!GROUPED) h = h * cs;
+      if (r0 + i < mrows) p.c[(int64_t)(r0 + i) * p.n + n] = __builtin_bit_cast(uint16_t, h);
+    }
+  }
+  return true;
+}
+
 struct NoWait {
   __device__ void operator()() const {}
 };
@@ -167,6 +243,12 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int s_prev;
   __shared__ uint64_t s_keys[kWaves][kMaxM];
+  // Every kernel argument the prologue needs, fetched in one round trip
+  // (left to itself the compiler loads the split fields, divides, and only
+  // then loads the pointers: two dependent kernarg fetches before the first
+  // weight load).
+  asm volatile("" ::"s"(p.a), "s"(p.b), "s"(p.s), "s"(p.counters), "s"(p.partial), "s"(p.m), "s"(p.n), "s"(p.k),
+               "s"(p.splits), "s"(p.kp_total));
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -387,6 +469,9 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
 #pragma unroll
   for (int i = 0; i < kDepth - 1; ++i)
     if (b + kDepth + i < nb) consume(bw[i], bs[i], b + kDepth + i);
+
+  // Wide tiles (each wave its own chunk): the wave hands off on its own.
+  if constexpr (EPI == EPI_STORE && CPW == kWaves) return wave_epilogue<GROUPED>(p, acc, chunk, split, 1);
 
   // ---- epilogue: accumulators -> LDS tile [mrows][256] fp32 ----
   __syncthreads();  // every wave is done with the staged A
