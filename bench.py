@@ -3,17 +3,20 @@
 
 Headline (``value``): the Marlin-layout W4A16 decode GEMV of BASELINE.json
 configs[1] at M=1 -- K=5120, N=17408, group 128 -- in GB/s of algorithmic
-bytes (K*N/2 + (K/128)*N*2 + M*K*2 + M*N*2 per call).  A "step" is one call.
-Inputs are resident in HBM before timing; the call sequence cycles through
-``--sets`` independent weight sets (>256 MB in total, so the 256 MB Infinity
-Cache cannot serve the weights) and is replayed from a HIP graph so the
-timed region measures back-to-back kernels, not Python launch overhead.
+bytes (K*N/2 + (K/128)*N*2 + M*K*2 + M*N*2 per call).  Inputs are resident in
+HBM before timing.  A *step* is one call on each of the ``sets`` independent
+weight sets (> 2x the 256 MB Infinity Cache together, so the cache cannot
+serve the weights): the calls of one step are captured once in a HIP graph,
+and ``--steps`` replays of it are timed with HIP events on the launch stream
+(``--warmup`` untimed replays first), so the timed region is
+``steps x sets`` back-to-back kernels.
 
 Extra fields report the other BASELINE configs: M=4/16 decode, the M=2048
-prefill GEMM in TFLOP/s (both shapes), the rowwise fallback sweep, and the
-64-layer decode-step projection sweep.  ``cpu_baseline`` times the CPU
-restatement of the reference's dequantise-then-matmul path on a bounded
-sample of the headline workload.
+prefill GEMM in TFLOP/s (both shapes), the rowwise fallback sweep, the
+64-layer decode-step projection sweep, and the streaming-read ceiling of the
+device (a kernel that only reads the same bytes).  ``cpu_baseline`` times a
+vectorised torch-CPU restatement of the dequantise-then-matmul arithmetic on
+the host's physical cores, on a bounded sample.
 """
 from __future__ import annotations
 
@@ -26,6 +29,7 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, vendor spec
+TRAFFIC_FILE = "profiles/marlin_gemv_m1_k5120_n17408_traffic.txt"
 FP16_DENSE_PEAK_TFLOPS = 2516.6  # 256 CU x 2.4 GHz x 4096 flop/clk, vendor spec
 MALL_BYTES = 256 * 1024 * 1024
 
@@ -78,12 +82,12 @@ class RowwiseProblem:
 
 
 def time_calls(torch, fn, n_sets, steps, warmup, use_graph=True):
-    """Runs `steps` calls cycling over `n_sets` sets; returns (elapsed_ms, steps_done).
+    """Times `steps` steps of one call per weight set (`n_sets` calls each);
+    returns (elapsed_ms, steps, calls).
 
-    With use_graph the calls of one cycle are captured once in a HIP graph and
+    With use_graph the calls of one step are captured once in a HIP graph and
     replayed; events bracket the replays on the launch stream."""
-    rounds = max(1, steps // n_sets)
-    warm_rounds = max(1, warmup // n_sets)
+    steps = max(1, int(steps))
     stream = torch.cuda.current_stream()
     if use_graph:
         side = torch.cuda.Stream()
@@ -98,22 +102,27 @@ def time_calls(torch, fn, n_sets, steps, warmup, use_graph=True):
         with torch.cuda.graph(graph, stream=side):
             for i in range(n_sets):
                 fn(i)
-        run_round = graph.replay
+        run_step = graph.replay
     else:
-        def run_round():
+        def run_step():
             for i in range(n_sets):
                 fn(i)
-    for _ in range(warm_rounds):
-        run_round()
+    for _ in range(max(1, int(warmup))):
+        run_step()
     torch.cuda.synchronize()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record(stream)
-    for _ in range(rounds):
-        run_round()
+    for _ in range(steps):
+        run_step()
     stop.record(stream)
     torch.cuda.synchronize()
-    return start.elapsed_time(stop), rounds * n_sets
+    return start.elapsed_time(stop), steps, steps * n_sets
+
+
+def calls_per_step_for(n_sets, calls):
+    """Steps (of `n_sets` calls) covering at least `calls` calls."""
+    return max(1, math.ceil(calls / n_sets))
 
 
 class DecodeStep:
@@ -124,7 +133,7 @@ class DecodeStep:
     17408->5120 through the SiLU-gated op on that `mixed` row -- the
     production call sequence (langburst/model.py:1414-1482).  W4 g128 random
     packed weights, all resident (about 10.9 GB).  fused_mlp: gate/up, SiLU
-    and down as one lb_marlin_mlp_fused call in its automatic mode (one launch
+    and down as one lb_marlin_mlp_fused call asking for one launch (mode 1; one launch
     for M = 2..16, the two launches at M = 1), whose output is bit-identical
     to the two calls."""
 
@@ -159,7 +168,7 @@ class DecodeStep:
             self.fws = torch.zeros((capi.marlin_mlp_fused_workspace_len(m, h, it),), dtype=torch.int32, device=dev)
             self.fscratch = torch.empty((capi.marlin_mlp_fused_scratch_bytes(m, h, it),), dtype=torch.uint8,
                                         device=dev)
-            self.launches_per_layer = 2 + capi.marlin_mlp_fused_launches(m, h, it, 128, 128)
+            self.launches_per_layer = 2 + capi.marlin_mlp_fused_launches(m, h, it, 128, 128, capi.MLP_ONE_LAUNCH)
         per_layer = (marlin_bytes(m, h, self.QKV) + marlin_bytes(m, self.O_IN, h) + marlin_bytes(m, h, 2 * it)
                      + marlin_bytes(m, it, h) + m * it * 2)  # the gated op reads [gate | up]: 2K halves per row
         self.bytes_per_step = per_layer * layers
@@ -172,7 +181,7 @@ class DecodeStep:
             lc.lowbit_marlin_gemm_out(*L["o"], self.x, self.o_out, self.ws, self.O_IN, 128)
             if self.fused_mlp:
                 st = self.capi.marlin_mlp_fused(self.x, *L["gate_up"], *L["down"], self.down_out, h, it, 128, 128,
-                                                self.fws, self.fscratch)
+                                                self.fws, self.fscratch, mode=self.capi.MLP_ONE_LAUNCH)
                 assert st == 0, self.capi.status_string(st)
             else:
                 lc.lowbit_marlin_gemm_out(*L["gate_up"], self.x, self.mixed, self.ws, h, 128)
@@ -204,6 +213,9 @@ def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5, fused_mlp=False):
            "bytes_per_step": ds.bytes_per_step, "weight_bytes_resident": ds.weight_bytes,
            "GB/s": round(ds.bytes_per_step / us / 1e3, 1),
            "frac_hbm": round(ds.bytes_per_step / us / 1e3 / HBM_PEAK_GBS, 4)}
+    if fused_mlp:  # the one-launch form's in-kernel waits must not have given up
+        st = ds.capi.marlin_mlp_fused_check(ds.fws)
+        res["one_launch_check"] = "ok" if st == 0 else ds.capi.status_string(st)
     del graph, ds
     torch.cuda.empty_cache()
     return res
@@ -213,73 +225,119 @@ def sets_for(bytes_per_set, minimum=8):
     return max(minimum, math.ceil(2.0 * MALL_BYTES / bytes_per_set))
 
 
-def _cpu_threads():
-    from threadpoolctl import threadpool_info
+def stream_ceiling(torch, dev, nbytes, n_sets, steps=30, wg_counts=(256, 512, 1024, 2048)):
+    """The streaming-read ceiling: lb_probe_stream_read over `nbytes` per launch
+    (the headline's algorithmic bytes), rotating over `n_sets` buffers like the
+    headline, at several grid sizes; the best is reported."""
+    from neurova_amd import capi
 
-    return max([t.get("num_threads", 1) for t in threadpool_info()] + [1])
+    nb = (nbytes + 15) // 16 * 16
+    bufs = [torch.randint(0, 2 ** 31, (nb // 4,), dtype=torch.int32, device=dev) for _ in range(n_sets)]
+    sink = torch.empty((max(wg_counts) * 4,), dtype=torch.int32, device=dev)
+    per_wg = {}
+    for wgs in wg_counts:
+        def call(i, wgs=wgs):
+            assert capi.probe_stream_read(bufs[i], sink, wgs) == 0
+        ms, _, calls = time_calls(torch, call, n_sets, steps, 3, True)
+        per_wg[wgs] = ms * 1e3 / calls
+    best = min(per_wg, key=per_wg.get)
+    us = per_wg[best]
+    del bufs, sink
+    torch.cuda.empty_cache()
+    return {"bytes_per_launch": nb, "workgroups": best, "us_per_launch": round(us, 3),
+            "GB/s": round(nb / us / 1e3, 1), "frac_hbm": round(nb / us / 1e3 / HBM_PEAK_GBS, 4),
+            "us_by_workgroups": {str(w): round(v, 3) for w, v in per_wg.items()}}
+
+
+def host_cpu():
+    """CPU model, physical cores and the cores this process may run on."""
+    model, sockets, per_socket = platform.processor() or platform.machine(), 1, 0
+    try:
+        import subprocess
+
+        out = subprocess.run(["lscpu"], capture_output=True, text=True, timeout=10).stdout
+        for line in out.splitlines():
+            key, _, val = line.partition(":")
+            key, val = key.strip(), val.strip()
+            if key == "Model name":
+                model = val
+            elif key == "Socket(s)":
+                sockets = int(val)
+            elif key == "Core(s) per socket":
+                per_socket = int(val)
+    except (OSError, ValueError):
+        pass
+    physical = sockets * per_socket or (os.cpu_count() or 1)
+    allowed = len(os.sched_getaffinity(0)) if hasattr(os, "sched_getaffinity") else (os.cpu_count() or 1)
+    return {"model": model, "physical_cores": physical, "allowed_cpus": allowed}
+
+
+def _timed(fn, budget_s, min_calls=3):
+    fn()
+    ts, t_end = [], time.perf_counter() + budget_s
+    while len(ts) < min_calls or time.perf_counter() < t_end:
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sum(ts) / len(ts), len(ts)
 
 
 def cpu_baseline(m, k, n, budget_s=12.0):
-    """CPU restatement of the dequantise-then-matmul reference path on the headline
-    shape (oracle package; the reference itself raises for Marlin on CPU,
-    ops.py:65-79), timed for about `budget_s` seconds."""
+    """The headline's dequantise-then-matmul arithmetic in vectorised torch-CPU
+    (oracle/torch_cpu.py: fp16 (q - 8) * s weights, fp32 matmul) on the host's
+    physical cores, timed for about `budget_s` seconds.  The reference itself
+    has no CPU Marlin path (ops.py:65-79 raises): this is a stated port of the
+    same arithmetic, not the reference's code."""
     import numpy as np
+    import torch
 
-    from oracle import lowbit_oracle as O
+    from oracle import torch_cpu as T
 
+    cpu = host_cpu()
+    threads = max(1, min(cpu["physical_cores"], cpu["allowed_cpus"]))
+    torch.set_num_threads(threads)
     rng = np.random.default_rng(0)
-    qw = rng.integers(-2 ** 31, 2 ** 31, size=(k // 16, 2 * n), dtype=np.int64).astype(np.int32)
-    s = (np.abs(rng.normal(0, 0.01, (k // 128, n))) + 1e-3).astype(np.float16)
-    x = rng.normal(0, 1, (m, k)).astype(np.float16)
-    O.marlin_gemm(x, qw, s, 128)  # warm-up
-    times = []
-    t_end = time.perf_counter() + budget_s
-    while len(times) < 3 or time.perf_counter() < t_end:
-        t0 = time.perf_counter()
-        O.marlin_gemm(x, qw, s, 128)
-        times.append(time.perf_counter() - t0)
-    sec = sum(times) / len(times)
-    threads = _cpu_threads()
+    qw = torch.from_numpy(rng.integers(-2 ** 31, 2 ** 31, size=(k // 16, 2 * n), dtype=np.int64).astype(np.int32))
+    s = torch.from_numpy((np.abs(rng.normal(0, 0.01, (k // 128, n))) + 1e-3).astype(np.float16))
+    x = torch.from_numpy(rng.normal(0, 1, (m, k)).astype(np.float16))
+    sec, calls = _timed(lambda: T.marlin_gemm(x, qw, s, 128), budget_s)
     return {
         "value": round(marlin_bytes(m, k, n) / sec / 1e9, 4),
         "unit": "GB/s",
         "cores": int(threads),
         "kind": "port",
-        "sample": f"{len(times)} full calls of the headline M={m} K={k} N={n} g128 in {sum(times):.1f} s "
-                  f"(numpy unpack + fp16 dequant single-threaded, float64 matmul on {threads} BLAS threads); "
-                  f"{sec * 1e3:.0f} ms/call",
-        "cpu": platform.processor() or platform.machine(),
+        "sample": f"{calls} full calls of the headline M={m} K={k} N={n} g128 ({sec * 1e3:.1f} ms/call): Marlin unpack, "
+                  "fp16 dequant and fp32 matmul in torch-CPU; the reference has no CPU Marlin path, this ports "
+                  "its arithmetic",
+        "cpu": cpu["model"], "physical_cores": cpu["physical_cores"], "allowed_cpus": cpu["allowed_cpus"],
     }
 
 
-def cpu_rowwise_cfg1(budget_s=4.0):
-    """the reference's CPU rowwise 4-bit GEMV (loader.py:427-465,
-    ops.py:16-44) restated in numpy, x [1,4096], W [4096,4096] g128: (a) dequant +
-    matmul per call, (b) matmul on pre-dequantised weights."""
-    import numpy as np
+def cpu_rowwise_cfg1(budget_s=6.0):
+    """the reference's CPU rowwise path (LowBitTensor.gemv's
+    CPU branch, loader.py:170-171 over dequantize_lowbit_rows, :427-465) in
+    vectorised torch-CPU on the physical cores, x [4096], W [4096, 4096] b4
+    g128, seed 0: (a) dequant + fp16 matmul per call, (b) the matmul alone on
+    the pre-dequantised fp16 matrix."""
+    import torch
 
     from oracle import lowbit_oracle as O
+    from oracle import torch_cpu as T
 
+    cpu = host_cpu()
+    threads = max(1, min(cpu["physical_cores"], cpu["allowed_cpus"]))
+    torch.set_num_threads(threads)
     _, packed, scales, x = O.make_rowwise_inputs(4096, 4096, 4, 128, batch=1, seed=0)
+    q, s, xv = torch.from_numpy(packed), torch.from_numpy(scales), torch.from_numpy(x[0])
     nbytes = rowwise_bytes(1, 4096, 4096, 4, 128)
-
-    def timed(fn):
-        fn()
-        ts, t_end = [], time.perf_counter() + budget_s / 2
-        while len(ts) < 3 or time.perf_counter() < t_end:
-            t0 = time.perf_counter()
-            fn()
-            ts.append(time.perf_counter() - t0)
-        return sum(ts) / len(ts), len(ts)
-
-    sec_a, na = timed(lambda: O.rowwise_gemv(packed, scales, x[0], 4096, 128, 4))
-    w = O.rowwise_dequant_f32(packed, scales, 4096, 128, 4)
-    xf = x[0].astype(np.float32)
-    sec_b, nb = timed(lambda: (w @ xf).astype(np.float16))
-    return {"dequant_matmul": {"us_per_call": round(sec_a * 1e6, 1), "GB/s": round(nbytes / sec_a / 1e9, 4), "calls": na},
-            "matmul_only_predequantised": {"us_per_call": round(sec_b * 1e6, 1), "GB/s": round(nbytes / sec_b / 1e9, 4),
-                                           "calls": nb},
-            "cores": int(_cpu_threads()), "kind": "port"}
+    sec_a, na = _timed(lambda: T.rowwise_gemv(q, s, xv, 4096, 128, 4), budget_s / 2)
+    dense = T.rowwise_dequant_rows(q, s, 4096, 128, 4)
+    sec_b, nb = _timed(lambda: torch.matmul(dense, xv), budget_s / 2)
+    return {"dequant_matmul": {"us_per_call": round(sec_a * 1e6, 1), "GB/s": round(nbytes / sec_a / 1e9, 4),
+                               "calls": na},
+            "matmul_only_predequantised": {"us_per_call": round(sec_b * 1e6, 1),
+                                           "GB/s": round(nbytes / sec_b / 1e9, 4), "calls": nb},
+            "cores": int(threads), "kind": "port", "impl": "torch-CPU (oracle/torch_cpu.py)", "cpu": cpu["model"]}
 
 
 def read_traffic(path):
@@ -372,8 +430,8 @@ def mlp_probe(torch, dev, calls=40):
 
         for name, fn, n_calls in (("two launches", pair, calls), ("one launch", fused, calls),
                                   ("streaming (fp32 numerics)", streaming, sets)):
-            ms, st = time_calls(torch, fn, sets, n_calls, sets, True)
-            log(f"[mlp-probe] M={m:2d} {name}: {ms * 1e3 / st:.2f} us per MLP")
+            ms, _, nc = time_calls(torch, fn, sets, calls_per_step_for(sets, n_calls), 1, True)
+            log(f"[mlp-probe] M={m:2d} {name}: {ms * 1e3 / nc:.2f} us per MLP")
         assert int(ws.abs().sum()) == 0
     del w
     torch.cuda.empty_cache()
@@ -382,8 +440,8 @@ def mlp_probe(torch, dev, calls=40):
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
-    ap.add_argument("--steps", type=int, default=3000)
-    ap.add_argument("--warmup", type=int, default=300)
+    ap.add_argument("--steps", type=int, default=300, help="timed steps (one call on each weight set per step)")
+    ap.add_argument("--warmup", type=int, default=30)
     ap.add_argument("--sets", type=int, default=0, help="weight sets to rotate (0 = enough to exceed 2x MALL)")
     ap.add_argument("--no-graph", action="store_true")
     ap.add_argument("--skip-cpu", action="store_true")
@@ -391,6 +449,8 @@ def main():
     ap.add_argument("--pmc-probe", action="store_true", help="run the counter-calibration probe and exit")
     ap.add_argument("--gemm-probe", action="store_true", help="run the prefill GEMM counter probe and exit")
     ap.add_argument("--mlp-probe", action="store_true", help="time the decode MLP (two launches / one launch) and exit")
+    ap.add_argument("--stream-probe", action="store_true",
+                    help="time the streaming-read ceiling over the headline's bytes and exit")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -416,6 +476,11 @@ def main():
     if args.mlp_probe:
         mlp_probe(torch, dev)
         return
+    if args.stream_probe:
+        pc = marlin_bytes(1, 5120, 17408)
+        r = stream_ceiling(torch, dev, pc, sets_for(pc), steps=max(1, args.steps // 10))
+        log(f"[stream-probe] {json.dumps(r)}")
+        return
     use_graph = not args.no_graph
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; graph={use_graph}")
 
@@ -426,10 +491,10 @@ def main():
     prob = MarlinProblem(torch, dev, m, k, n, n_sets, seed=1)
     log(f"[bench] headline M={m} K={k} N={n}: {n_sets} weight sets ({n_sets * per_call / 2**20:.0f} MiB)")
     torch.cuda.synchronize()
-    ms, steps = time_calls(torch, lambda i: prob.call(lc, i), n_sets, args.steps, args.warmup, use_graph)
-    us_per = ms * 1e3 / steps
+    ms, steps, calls = time_calls(torch, lambda i: prob.call(lc, i), n_sets, args.steps, args.warmup, use_graph)
+    us_per = ms * 1e3 / calls
     gbs = per_call / (us_per * 1e-6) / 1e9
-    log(f"[bench] headline {us_per:.2f} us/call, {gbs:.1f} GB/s")
+    log(f"[bench] headline {us_per:.2f} us/call, {gbs:.1f} GB/s ({steps} steps x {n_sets} calls)")
     del prob
     torch.cuda.empty_cache()
 
@@ -441,29 +506,35 @@ def main():
         "steps": steps,
         "warmup": args.warmup,
         "ms_per_step": round(ms / steps, 6),
+        "calls_per_step": n_sets,
+        "timed_calls": calls,
         "higher_is_better": True,
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp16 (int4 weights, fp32 accumulate)",
         "data": "synthetic (uniform int4 codes, |N(0,0.01)|+1e-3 fp16 scales, N(0,1) fp16 activations)",
-        "config": {"workload": f"marlin_w4a16_gemv M=1 K=5120 N=17408 g128, {n_sets} rotating weight sets"
-                               + (", hipGraph replay" if use_graph else ", eager launches"),
+        "config": {"workload": f"marlin_w4a16_gemv M=1 K=5120 N=17408 g128; a step is one call on each of "
+                               f"{n_sets} rotating weight sets" + (", hipGraph replay" if use_graph else ", eager launches"),
                    "m": m, "k": k, "n": n, "group_size": 128, "weight_sets": n_sets},
         "roofline": {"bound": "hbm", "achieved": round(gbs, 2), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(gbs / HBM_PEAK_GBS, 4),
-                     "traffic": read_traffic(os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                                                          "marlin_gemv_m1_k5120_n17408_traffic.txt")),
-                     "bytes_per_launch": per_call, "us_per_launch": round(us_per, 3)},
+                     "traffic": read_traffic(os.path.join(os.path.dirname(os.path.abspath(__file__)), TRAFFIC_FILE)),
+                     "traffic_source": f"{TRAFFIC_FILE} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, "
+                                       "calibrated on a copy kernel; not measured in this run)",
+                     "bytes_per_launch": per_call, "us_per_launch": round(us_per, 3),
+                     "timing": "HIP events on the launch stream around the graph replays"},
     }
 
     if not args.skip_extra:
-        extra = {}
+        extra = {"stream_read_ceiling": stream_ceiling(torch, dev, per_call, n_sets)}
+        log(f"[bench] streaming-read ceiling over {per_call} B: {extra['stream_read_ceiling']['us_per_launch']:.2f} us, "
+            f"{extra['stream_read_ceiling']['GB/s']:.1f} GB/s")
         for mm in (4, 16):
             pc = marlin_bytes(mm, k, n)
             ns = sets_for(pc)
             pr = MarlinProblem(torch, dev, mm, k, n, ns, seed=2 + mm)
-            ms2, st2 = time_calls(torch, lambda i: pr.call(lc, i), ns, 600, 60, use_graph)
-            u = ms2 * 1e3 / st2
+            ms2, _, nc2 = time_calls(torch, lambda i: pr.call(lc, i), ns, calls_per_step_for(ns, 600), 5, use_graph)
+            u = ms2 * 1e3 / nc2
             extra[f"marlin_gemv_m{mm}"] = {"us_per_call": round(u, 3), "GB/s": round(pc / u / 1e3, 1),
                                            "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4)}
             log(f"[bench] M={mm}: {u:.2f} us, {pc / u / 1e3:.1f} GB/s")
@@ -473,8 +544,8 @@ def main():
             pr = MarlinProblem(torch, dev, mm, kk, nn, 2, seed=11)
             # 40 untimed calls (about 14 ms) first: the engine clock settles
             # under sustained MFMA load; the first few calls run faster or slower
-            ms2, st2 = time_calls(torch, lambda i: pr.call(lc, i), 2, 40, 40, use_graph)
-            u = ms2 * 1e3 / st2
+            ms2, _, nc2 = time_calls(torch, lambda i: pr.call(lc, i), 2, 20, 20, use_graph)
+            u = ms2 * 1e3 / nc2
             tf = 2.0 * mm * kk * nn / (u * 1e-6) / 1e12
             extra[f"marlin_gemm_m2048_k{kk}_n{nn}"] = {"us_per_call": round(u, 2), "TFLOP/s": round(tf, 1),
                                                        "frac_fp16_peak": round(tf / FP16_DENSE_PEAK_TFLOPS, 4)}
@@ -485,8 +556,8 @@ def main():
                 pc = rowwise_bytes(1, 17408, 5120, bits, g)
                 ns = sets_for(pc)
                 pr = RowwiseProblem(torch, dev, 17408, 5120, bits, g, ns, seed=bits * g)
-                ms2, st2 = time_calls(torch, lambda i: pr.call(lc, i), ns, 400, 40, use_graph)
-                u = ms2 * 1e3 / st2
+                ms2, _, nc2 = time_calls(torch, lambda i: pr.call(lc, i), ns, calls_per_step_for(ns, 400), 5, use_graph)
+                u = ms2 * 1e3 / nc2
                 extra[f"rowwise_b{bits}_g{g}"] = {"us_per_call": round(u, 3), "GB/s": round(pc / u / 1e3, 1),
                                                   "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4)}
                 log(f"[bench] rowwise b{bits} g{g}: {u:.2f} us, {pc / u / 1e3:.1f} GB/s")
@@ -494,8 +565,8 @@ def main():
         pc = rowwise_bytes(1, 4096, 4096, 4, 128)
         ns = sets_for(pc)
         pr = RowwiseProblem(torch, dev, 4096, 4096, 4, 128, ns, seed=5)
-        ms2, st2 = time_calls(torch, lambda i: pr.call(lc, i), ns, 400, 40, use_graph)
-        u = ms2 * 1e3 / st2
+        ms2, _, nc2 = time_calls(torch, lambda i: pr.call(lc, i), ns, calls_per_step_for(ns, 400), 5, use_graph)
+        u = ms2 * 1e3 / nc2
         extra["rowwise_cfg1_b4_4096"] = {"us_per_call": round(u, 3), "GB/s": round(pc / u / 1e3, 1),
                                          "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4)}
         del pr
@@ -505,8 +576,8 @@ def main():
         pc = rowwise_bytes(1, 5120, 96, 4, 128)
         ns = sets_for(pc, minimum=64)
         pr = RowwiseProblem(torch, dev, 5120, 96, 4, 128, ns, seed=96)
-        ms2, st2 = time_calls(torch, lambda i: pr.call(lc, i), ns, 640, 64, use_graph)
-        u = ms2 * 1e3 / st2
+        ms2, _, nc2 = time_calls(torch, lambda i: pr.call(lc, i), ns, calls_per_step_for(ns, 640), 2, use_graph)
+        u = ms2 * 1e3 / nc2
         extra["rowwise_in_proj_ba_b4_g128_96x5120"] = {"us_per_call": round(u, 3), "GB/s": round(pc / u / 1e3, 1),
                                                        "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4)}
         del pr
@@ -516,9 +587,9 @@ def main():
         emb_q = torch.randint(0, 256, (emb_rows, emb_cols // 2), dtype=torch.uint8, device=dev, generator=gen)
         emb_s = (torch.randn((emb_rows, emb_cols // 128), device=dev, generator=gen) * 0.01).abs_().add_(1e-3).half()
         tokens = [torch.randint(0, emb_rows, (1,), device=dev, generator=gen) for _ in range(64)]
-        ms2, st2 = time_calls(torch, lambda i: lc.lowbit_row_dequant(emb_q, emb_s, tokens[i], emb_cols, 128, 4),
-                              64, 640, 64, use_graph)
-        u = ms2 * 1e3 / st2
+        ms2, _, nc2 = time_calls(torch, lambda i: lc.lowbit_row_dequant(emb_q, emb_s, tokens[i], emb_cols, 128, 4),
+                              64, 10, 1, use_graph)
+        u = ms2 * 1e3 / nc2
         pc = emb_cols // 2 + emb_cols // 128 * 2 + emb_cols * 2 + 8
         extra["row_dequant_embedding_b4_248320x5120"] = {"us_per_call": round(u, 3), "bytes_per_call": pc}
         log(f"[bench] in_proj_ba {extra['rowwise_in_proj_ba_b4_g128_96x5120']['us_per_call']:.2f} us, "

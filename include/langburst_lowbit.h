@@ -35,7 +35,8 @@ enum lb_status {
   LB_ERR_ALIGN = 4,      /* a pointer is not aligned as the kernels require */
   LB_ERR_WORKSPACE = 5,  /* workspace shorter than required */
   LB_ERR_SCRATCH = 6,    /* scratch buffer shorter than lb_marlin_scratch_bytes() */
-  LB_ERR_HIP = 7         /* the HIP runtime reported an error at launch */
+  LB_ERR_HIP = 7,        /* the HIP runtime reported an error at launch */
+  LB_ERR_HANDOFF = 8     /* lb_marlin_mlp_fused_check: an in-kernel wait gave up (output not valid) */
 };
 
 typedef void* lb_stream_t; /* hipStream_t */
@@ -163,14 +164,16 @@ int lb_marlin_mlp_streaming(const int32_t* gate_up_qweight, const uint16_t* gate
  * _fused_marlin_down, loader.py:337-368): bit-identical to lb_marlin_gemm followed
  * by lb_marlin_gemm_silu_packed, in every mode.
  * No reference op: replaces that pair of calls.
- * mode: 0 auto (one launch for batch 2..16 when every workgroup of it fits on
- *       the device at once, else the two launches), 1 one launch whenever it
- *       fits, 2 always the two launches.  lb_marlin_mlp_fused_launches says
- *       which a call takes.
+ * mode: 0 auto and 2: the two launches; 1: one launch when every workgroup
+ *       of it fits on the device at once (else the two launches).  The one
+ *       launch hands activations between workgroups with bounded waits that
+ *       need all of its workgroups resident; a wait that gives up (another
+ *       kernel holding compute units) leaves that call's output not valid,
+ *       so it runs only when the caller asks for it and checks the call with
+ *       lb_marlin_mlp_fused_check.  lb_marlin_mlp_fused_launches says which
+ *       form a call takes.
  * workspace: int32 [lb_marlin_mlp_fused_workspace_len()], zero on entry, left
- *            zero (entry 1 stays 1 if a hand-off wait gave up: the
- *            output is then not valid, and the workspace must be zeroed
- *            again before the next call).
+ *            zero (entry 1 stays 1 if a one-launch wait gave up).
  * scratch:   lb_marlin_mlp_fused_scratch_bytes() bytes, 256-byte aligned.
  * Calls that share a workspace must not overlap. */
 size_t lb_marlin_mlp_fused_scratch_bytes(int64_t batch, int64_t hidden, int64_t intermediate);
@@ -184,6 +187,15 @@ int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qweight, const
                         int64_t gate_group_size, int64_t down_group_size, int32_t mode,
                         int32_t* workspace, int64_t workspace_len,
                         void* scratch, size_t scratch_bytes, lb_stream_t stream);
+/* Waits for `stream`, then reads the workspace of lb_marlin_mlp_fused calls:
+ * LB_ERR_HANDOFF if a one-launch wait gave up since the workspace was last
+ * checked (the workspace, workspace_len entries, is then zeroed, so the next
+ * call starts clean), else LB_OK.  Synchronises; no reference counterpart. */
+int lb_marlin_mlp_fused_check(int32_t* workspace, int64_t workspace_len, lb_stream_t stream);
+/* Test hook: polls a one-launch wait makes before it gives up (default
+ * 262144; values < 1 restore the default).  Lets a test force the give-up
+ * path from the host with every kernel still ending normally. */
+void lb_marlin_mlp_fused_set_spin_limit(int32_t polls);
 
 /* Dense fp16 W[N, K] = fp16((q - 8) * s) (or q - 8 for per-column scales),
  * bit-exact with the reference's in-kernel dequant (csrc/marlin_cuda_kernel.cu:131-159).
@@ -191,6 +203,13 @@ int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qweight, const
  * reference's scalar reader csrc/marlin_mlp_stream.cu:109-133. */
 int lb_marlin_dequant(const int32_t* B, const uint16_t* s, uint16_t* w_nk,
                       int64_t prob_n, int64_t prob_k, int64_t groupsize, lb_stream_t stream);
+
+/* ---------------- Measurement probe (no reference counterpart) ----------------
+ * Reads `bytes` (a multiple of 16) of device memory at `src` with 16-byte
+ * loads over `workgroups` workgroups of 256 threads, each a contiguous range,
+ * and writes one word per wave to sink[workgroups * 4]: the streaming-read
+ * ceiling that the bandwidth-bound kernels are compared with. */
+int lb_probe_stream_read(const void* src, size_t bytes, uint32_t* sink, int32_t workgroups, lb_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -24,6 +24,7 @@ LB_ERR_ALIGN = 4
 LB_ERR_WORKSPACE = 5
 LB_ERR_SCRATCH = 6
 LB_ERR_HIP = 7
+LB_ERR_HANDOFF = 8
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -44,10 +45,13 @@ _SIGNATURES = {
     "lb_marlin_mlp_scratch_bytes": ([I64, I64, I64], SZ),
     "lb_marlin_mlp_streaming": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, SZ, P], ctypes.c_int),
     "lb_marlin_dequant": ([P, P, P, I64, I64, I64, P], ctypes.c_int),
+    "lb_probe_stream_read": ([P, SZ, P, I32, P], ctypes.c_int),
     "lb_marlin_mlp_fused_scratch_bytes": ([I64, I64, I64], SZ),
     "lb_marlin_mlp_fused_workspace_len": ([I64, I64, I64], I64),
     "lb_marlin_mlp_fused_launches": ([I64, I64, I64, I64, I64, I32], ctypes.c_int),
     "lb_marlin_mlp_fused": ([P, P, P, P, P, P, I64, I64, I64, I64, I64, I32, P, I64, P, SZ, P], ctypes.c_int),
+    "lb_marlin_mlp_fused_check": ([P, I64, P], ctypes.c_int),
+    "lb_marlin_mlp_fused_set_spin_limit": ([I32], None),
 }
 
 
@@ -173,6 +177,19 @@ def marlin_mlp_fused(x, gu_q, gu_s, d_q, d_s, out, hidden, intermediate, gg, dg,
                                      _ptr(scratch), nbytes, _stream(x))
 
 
+def marlin_mlp_fused_check(workspace) -> int:
+    return lib().lb_marlin_mlp_fused_check(_ptr(workspace), workspace.numel(), _stream(workspace))
+
+
+def marlin_mlp_fused_set_spin_limit(polls: int) -> None:
+    lib().lb_marlin_mlp_fused_set_spin_limit(int(polls))
+
+
 def marlin_dequant(b, s, w_nk, k, group_size) -> int:
     n = b.shape[1] // 2
     return lib().lb_marlin_dequant(_ptr(b), _ptr(s), _ptr(w_nk), n, k, group_size, _stream(w_nk))
+
+
+def probe_stream_read(src, sink, workgroups) -> int:
+    return lib().lb_probe_stream_read(_ptr(src), src.numel() * src.element_size(), _ptr(sink), int(workgroups),
+                                      _stream(src))

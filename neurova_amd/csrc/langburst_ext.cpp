@@ -310,17 +310,17 @@ void lowbit_marlin_mlp_streaming_out(torch::Tensor gate_up_qweight, torch::Tenso
 
 // The decode MLP the reference's _fused_marlin_down runs as two ops
 // (langburst/adapters/qwen36_impl/model.py:1460-1470: gate/up GEMM, then the
-// SiLU-packed down GEMM), as one call: one kernel launch for batch 2..16 in
-// mode 0, the same two launches otherwise.  The result is bit-identical to the
-// two ops.  `workspace` is int32, zero on entry, and left zero, except that
-// entry 1 stays 1 if the in-kernel hand-off gave up waiting: the output of that
-// call is then not valid and the workspace must be zeroed again.  Nothing
-// here synchronises, so a caller that wants the check reads entry 1 after the
-// stream has finished.
+// SiLU-packed down GEMM), as one call, bit-identical to the two ops.  Mode 0
+// (default) and 2 run the two launches; mode 1 runs one kernel launch where it
+// fits, whose in-kernel waits can give up when other work holds compute units
+// (the output of that call is then not valid).  check=True synchronises after
+// the call and raises RuntimeError if that happened, after zeroing the
+// workspace so that the next call starts clean.  `workspace` is int32, zero on
+// entry and left zero.
 void lowbit_marlin_mlp_fused_out(torch::Tensor gate_up_qweight, torch::Tensor gate_up_scales,
                                  torch::Tensor down_qweight, torch::Tensor down_scales, torch::Tensor x,
                                  torch::Tensor out, torch::Tensor workspace, int64_t hidden, int64_t intermediate,
-                                 int64_t gate_group_size, int64_t down_group_size, int64_t mode) {
+                                 int64_t gate_group_size, int64_t down_group_size, int64_t mode, bool check) {
   LB_CHECK_DEV(gate_up_qweight); LB_CHECK_DEV(gate_up_scales); LB_CHECK_DEV(down_qweight); LB_CHECK_DEV(down_scales);
   LB_CHECK_DEV(x); LB_CHECK_DEV(out); LB_CHECK_DEV(workspace);
   LB_CHECK_CONTIG(gate_up_qweight); LB_CHECK_CONTIG(gate_up_scales); LB_CHECK_CONTIG(down_qweight);
@@ -359,6 +359,12 @@ void lowbit_marlin_mlp_fused_out(torch::Tensor gate_up_qweight, torch::Tensor ga
                             intermediate, gate_group, down_group, (int32_t)mode, workspace.data_ptr<int32_t>(),
                             workspace.numel(), scratch.data_ptr(), (size_t)scratch.numel(), stream_of(x)),
         "lowbit_marlin_mlp_fused_out");
+  if (check) {
+    const int st = lb_marlin_mlp_fused_check(workspace.data_ptr<int32_t>(), workspace.numel(), stream_of(x));
+    TORCH_CHECK(st != LB_ERR_HANDOFF, "lowbit_marlin_mlp_fused_out: the one-launch hand-off gave up waiting; the "
+                "output of this call is not valid (workspace zeroed)");
+    lb_ok(st, "lowbit_marlin_mlp_fused_out check");
+  }
 }
 
 // Dense fp16 W[N, K] of a Marlin tensor (no reference op; the reference's
@@ -420,10 +426,10 @@ PYBIND11_MODULE(langburst_cuda, m) {
   m.def("lowbit_marlin_dequant", &lowbit_marlin_dequant, "Dense fp16 W[N, K] of a Marlin tensor",
         py::arg("qweight"), py::arg("scales"), py::arg("cols"), py::arg("group_size"));
   m.def("lowbit_marlin_mlp_fused_out", &lowbit_marlin_mlp_fused_out,
-        "Marlin W4A16 decode MLP: down(SiLU(gate) * up) of x, one launch for batch 2..16 in mode 0",
+        "Marlin W4A16 decode MLP: down(SiLU(gate) * up) of x; mode 1 asks for one launch, check=True verifies it",
         py::arg("gate_up_qweight"), py::arg("gate_up_scales"), py::arg("down_qweight"), py::arg("down_scales"),
         py::arg("x"), py::arg("out"), py::arg("workspace"), py::arg("hidden"), py::arg("intermediate"),
-        py::arg("gate_group_size"), py::arg("down_group_size"), py::arg("mode") = 0);
+        py::arg("gate_group_size"), py::arg("down_group_size"), py::arg("mode") = 0, py::arg("check") = false);
   m.def("lowbit_marlin_mlp_fused_workspace_len",
         [](int64_t batch, int64_t hidden, int64_t intermediate) {
           return lb_marlin_mlp_fused_workspace_len(batch, hidden, intermediate);

@@ -6,6 +6,7 @@
 
 #include <algorithm>
 
+#include <atomic>
 #include <mutex>
 
 #include "marlin_gemm.hpp"
@@ -171,10 +172,7 @@ struct Plan {
   size_t keys_bytes = 0;
 };
 
-#ifndef LB_SKINNY_WGS_PER_CU
-#define LB_SKINNY_WGS_PER_CU 2    // decode workgroups resident per CU (register-limited)
-#endif
-constexpr int kSkinnyWGsPerCU = LB_SKINNY_WGS_PER_CU;
+constexpr int kSkinnyWGsPerCU = 2;  // decode workgroups resident per CU (register-limited)
 constexpr int kGemmMaxTailSplits = 16;
 constexpr int kSkinnyMaxSplits = 8;  // decode: beyond this, narrower tiles instead
 constexpr size_t kSkinnyMaxX = 48 * 1024;
@@ -250,11 +248,7 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
   // needs more than kSkinnyMaxSplits k splits to fill the chip: then 2 or 1
   // chunks, whose waves share the workgroup's k range.
   int cpw = 0, s = 0;
-#ifdef LB_SKINNY_CPW
-  constexpr int kCpwWidest = LB_SKINNY_CPW, kCpwNarrowest = LB_SKINNY_CPW;  // schedule sweeps only
-#else
   constexpr int kCpwWidest = 4, kCpwNarrowest = 1;
-#endif
   if (m <= skinny::kMaxM) {
     for (int c = kCpwWidest; c >= kCpwNarrowest; c /= 2) {
       const int sc = skinny_splits(m, n, k, workspace_len, c);
@@ -273,19 +267,14 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
     pl.splits = s;
     const int max_groups = (groups + s - 1) / s;
     pl.x_bytes = (size_t)max_groups * 128 * (size_t)m * 2;  // staged A slice (at most kSkinnyMaxX)
-    // + the zero entry + the bias corrections [group][16] fp32
-    const size_t stage = pl.x_bytes + 16 + (size_t)max_groups * skinny::kMaxM * 4;
+    const size_t stage = pl.x_bytes + 16;                    // + the zero entry
     pl.lds = std::max(stage, (size_t)m * skinny::kCols * 4);
     pl.partial_bytes = pl.splits > 1 ? align_up((size_t)pl.splits * (size_t)m * (size_t)n * 4) : 0;
   } else {
     pl.skinny = false;
     // 128-row tiles (two workgroups per CU) where M fills them; the SiLU-gated
     // variant keeps 64-row tiles (its A staging registers leave no room).
-#ifdef LB_GEMM_MB
-    pl.mb = (LB_GEMM_MB == 8 && am != gemm::A_PLAIN) ? 4 : LB_GEMM_MB;
-#else
     pl.mb = (m >= 128 && am == gemm::A_PLAIN) ? 8 : (m > 32 ? 4 : 2);
-#endif
     const int64_t bm = 16 * pl.mb;
     pl.n_mb = (int)((m + bm - 1) / bm);
     const int64_t tiles = (int64_t)pl.n_cg * pl.n_mb;
@@ -303,9 +292,6 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
       const int s_mem = std::min(std::min(s_fill, s_cap), groups);
       if (s_mem > s) s = s_mem;
     }
-#ifdef LB_GEMM_TAIL_SPLITS
-    if (tail > 0) s = LB_GEMM_TAIL_SPLITS < groups ? LB_GEMM_TAIL_SPLITS : groups;
-#endif
     if (s > 1 && workspace_len < 1 + tail) s = 1;
     // partials are addressed through a 32-bit buffer resource
     while (s > 1 && (size_t)tail * s * 16 * pl.mb * gemm::kThreads * 4 >= ((size_t)1 << 31)) --s;
@@ -446,6 +432,7 @@ extern "C" const char* lb_status_string(int status) {
     case LB_ERR_WORKSPACE: return "workspace too small";
     case LB_ERR_SCRATCH: return "scratch too small";
     case LB_ERR_HIP: return "HIP runtime error";
+    case LB_ERR_HANDOFF: return "in-kernel hand-off gave up; output not valid";
     default: return "unknown status";
   }
 }
@@ -623,11 +610,13 @@ int resident_per_cu(FusedKernel fn, size_t lds) {
   return v;
 }
 
-// Launch modes of lb_marlin_mlp_fused.  Auto: one launch from batch 2 on (at
-// batch 1 the fused kernel measured no faster than the two launches in a
-// graph-captured decode step; from batch 4 on it is, as its down phase stages
-// plain activations instead of SiLU-gating [g | u]).
+// Launch modes of lb_marlin_mlp_fused.  Auto takes the two launches: the one
+// launch (faster from batch 4 on, where its down phase stages plain
+// activations instead of SiLU-gating [g | u]) relies on bounded in-kernel
+// waits, so it runs only when the caller asks for it (mode 1).
 enum { kMlpAuto = 0, kMlpOne = 1, kMlpTwo = 2 };
+
+std::atomic<int> g_mlp_spin_limit{mlp::kSpinLimit};
 
 // occupancy == false: plan the layouts only (no device query; two launches).
 FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g1, bool g2, int mode,
@@ -635,7 +624,7 @@ FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g
   FusedMlpPlan p;
   p.up = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN);
   p.down = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED);
-  const bool wanted = mode == kMlpOne || (mode == kMlpAuto && batch >= 2);
+  const bool wanted = mode == kMlpOne;
   if (p.up.skinny && p.up.cpw >= 2 && p.down.skinny && p.down.splits <= mlp::kMaxSplits) {
     p.wgs = std::max(p.up.n_cg * p.up.splits, p.down.n_cg * p.down.splits);
     p.lds = std::max(p.up.lds, p.down.lds);
@@ -758,7 +747,27 @@ extern "C" int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qwe
   d.m = (int)batch; d.n = (int)hidden; d.k = (int)intermediate; d.splits = pl.down.splits;
   d.kp_total = (int)(intermediate / 32); d.n_cg = pl.down.n_cg;
   f.ws = workspace;
+  f.spin_limit = g_mlp_spin_limit.load(std::memory_order_relaxed);
   hipLaunchKernelGGL(fused_kernel(g1, g2, pl.up.cpw, pl.down.cpw), dim3((unsigned)pl.wgs), dim3(skinny::kThreads),
                      pl.lds, st, f);
   return lbh::launch_status();
+}
+
+extern "C" int lb_marlin_mlp_fused_check(int32_t* workspace, int64_t workspace_len, lb_stream_t stream) {
+  if (!workspace || workspace_len < 2) return LB_ERR_ARG;
+  hipStream_t st = (hipStream_t)stream;
+  int32_t flag = 0;
+  if (hipStreamSynchronize(st) != hipSuccess) return LB_ERR_HIP;
+  if (hipMemcpy(&flag, workspace + 1, sizeof(flag), hipMemcpyDeviceToHost) != hipSuccess) return LB_ERR_HIP;
+  if (flag == 0) return LB_OK;
+  // a late producer may have counted a tile after its split's counters were
+  // reset: clear every entry, then report the call
+  if (hipMemsetAsync(workspace, 0, (size_t)workspace_len * sizeof(int32_t), st) != hipSuccess ||
+      hipStreamSynchronize(st) != hipSuccess)
+    return LB_ERR_HIP;
+  return LB_ERR_HANDOFF;
+}
+
+extern "C" void lb_marlin_mlp_fused_set_spin_limit(int32_t polls) {
+  g_mlp_spin_limit.store(polls >= 1 ? polls : mlp::kSpinLimit, std::memory_order_relaxed);
 }

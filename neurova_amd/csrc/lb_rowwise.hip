@@ -189,14 +189,8 @@ __global__ __launch_bounds__(kThreads) void rowwise_fast_kernel(Params p) {
 // arithmetic results below 2^-14 are flushed to zero here.)  Each wave
 // computes R rows (of NW matrices) from one LDS read of the activations.
 // ---------------------------------------------------------------------------
-#ifndef LB_RW_LDS_WAVES
-#define LB_RW_LDS_WAVES 8
-#endif
-#ifndef LB_RW_LDS_ROWS
-#define LB_RW_LDS_ROWS 1
-#endif
-constexpr int kLdsWaves = LB_RW_LDS_WAVES;         // waves (rows x R) per workgroup
-constexpr int kLdsRows = LB_RW_LDS_ROWS;           // rows per wave (one matrix)
+constexpr int kLdsWaves = 8;                       // waves (rows x R) per workgroup
+constexpr int kLdsRows = 1;                        // rows per wave (one matrix)
 constexpr int kLdsThreads = kLdsWaves * kWave;
 constexpr int kLdsUnitBytes = 68;                  // 16 staged pair words + the unit's zero-point share
 constexpr int64_t kLdsMaxBytes = 64 * 1024;

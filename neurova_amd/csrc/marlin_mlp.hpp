@@ -26,9 +26,10 @@
 // kernel only when the instantiation's occupancy allows it and otherwise runs
 // the two projections.  Each wait is bounded: a workgroup that has polled
 // kSpinLimit times records a fault flag (workspace entry 1) and goes on, so a
-// launch always ends.  After such a fault a late producer may still count a
-// tile once its split's counters were reset, so the caller must zero the
-// workspace again before the next launch.
+// launch always ends.  The output of such a launch is not valid, and a late
+// producer may still count a tile once its split's counters were reset: the
+// host entry point runs this kernel only when the caller asks for it, and
+// lb_marlin_mlp_fused_check reports the flag and zeroes the workspace.
 
 #pragma once
 #include "marlin_skinny.hpp"
@@ -36,7 +37,7 @@
 namespace lb {
 namespace mlp {
 
-constexpr int kSpinLimit = 1 << 18;  // polls; each waits for its device-scope load, then sleeps 128 cycles
+constexpr int kSpinLimit = 1 << 18;  // default polls; each waits for its device-scope load, then sleeps 128 cycles
 constexpr int kLineInts = 32;        // one 128-byte line per counter
 constexpr int kMaxSplits = 64;       // down k splits the counters cover
 // workspace layout (int32): [1] fault flag; ready[s] at kReadyBase + kLineInts * s,
@@ -49,6 +50,7 @@ struct FusedParams {
   skinny::Params up;    // gate_up projection (EPI_ACT), N = 2 * intermediate
   skinny::Params down;  // down projection (A_HANDOFF), K = intermediate
   int32_t* ws;          // kSyncWorkspace entries, zero on entry and on exit
+  int spin_limit;       // polls before a wait gives up (kSpinLimit unless a test lowers it)
 };
 
 // The down split whose k range holds scale group `grp`: split s covers groups
@@ -77,7 +79,7 @@ __device__ __forceinline__ void wait_ready(const FusedParams& f, int s, int expe
     int32_t* ready = f.ws + kReadyBase + kLineInts * s;
     int spins = 0;
     while (__hip_atomic_load(ready, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) < expected) {
-      if (++spins > kSpinLimit) {
+      if (++spins > f.spin_limit) {
         __hip_atomic_store(f.ws + 1, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
         break;
       }

@@ -24,15 +24,12 @@
 // and 4g'+8+{0..3} of row p.  Lane l loads only slot 4c+2g'+h, so the 32
 // lanes of a row fetch its 512 bytes once; the other slot of the pair is in
 // lane l^8 and arrives by a DPP row rotation, and one v_perm_b32 gathers the
-// four bytes the lane uses.  Dequant is one v_and_or_b32 per fp16 pair, which
-// yields the exact biased values 1024 + q (k = 0..7 of a row, low nibbles) and
-// 1024 + 16q (k = 8..15, high nibbles); the A slice is staged with its
-// k = 8..15 halves scaled by 1/16, and each scale group's MFMAs start from
-// -(1032 * sum of the low-half activations + 1152 * sum of the staged high-half
-// ones), which removes the bias and leaves the sum of x * (q - 8) accumulated
-// in fp32.  The group's scale then multiplies that fp32 sum once
-// (the reference rounds each fp16 (q-8)*s before the MMA; the two differ by
-// that rounding, far inside fp16 output precision).
+// four bytes the lane uses.  Dequant per fp16 pair: one v_and_or_b32 gives
+// the biased 1024 + q (k = 0..7 of a row, low nibbles) or 1024 + 16q
+// (k = 8..15, high nibbles), one packed add (or fma by 1/16) makes it the
+// exact q - 8, and one packed multiply by the group's scale gives the
+// reference's fp16 (q - 8) * s, rounded as marlin_cuda_kernel.cu:131-159
+// rounds it; the MFMA then accumulates exact products in fp32.
 //
 // Latency.  The activation slice of the workgroup's k range is staged once in
 // LDS in fragment order ([k/32][4 k-groups][m] x 16 bytes, SiLU-gated
@@ -60,14 +57,7 @@ constexpr int kCols = 64 * kWaves;      // 256 columns per workgroup
 constexpr int kMaxM = 16;               // rows of the MFMA tile
 constexpr int kSteps = 4;               // 32-k steps per batch (one scale group)
 constexpr int kStageUnroll = 8;         // A staging: 16-byte items in flight per thread
-#ifndef LB_SKINNY_DEPTH
-#define LB_SKINNY_DEPTH 2
-#endif
-constexpr int kDepth = LB_SKINNY_DEPTH;  // weight batches in flight
-
-#ifndef LB_STREAM_LOADS
-#define LB_STREAM_LOADS 0               // non-temporal weight loads (measured slower)
-#endif
+constexpr int kDepth = 2;               // weight batches in flight
 
 // A_HANDOFF: plain fp16 A written earlier in the same launch by other
 // workgroups (the fused MLP's activations), read with device-coherent loads.
@@ -287,15 +277,13 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   const NibConsts nk = nib_consts();
 
   // LDS: staged A in fragment order, entry (kp, g, m) = 16 bytes holding
-  // x[m][32kp + 16(g>>1) + 4(g&1) + {0..3}] and, scaled by 1/16, the same +8;
-  // then one zero entry (read by the lanes of rows >= M), then the bias
-  // correction of each scale group of the slice, [group][16 rows] fp32.
+  // x[m][32kp + 16(g>>1) + 4(g&1) + {0..3}] and the same + 8, then one zero
+  // entry (read by the lanes of rows >= M).
   u32x4* afr = reinterpret_cast<u32x4*>(smem);
   const int k0 = kp0 * 32;
   const int octs = nkp * 4;            // 8-half runs per row of the slice
   const int items = octs * mrows;
   const int n_frag = nkp * 4 * mrows;  // staged entries; afr[n_frag] is the zero entry
-  float* corr = reinterpret_cast<float*>(afr + n_frag + 1);
   const int64_t a_row_stride = AM == A_SILU_PACKED ? 2 * (int64_t)p.k : (int64_t)p.k;
   const __amdgpu_buffer_rsrc_t ra = buffer_of(p.a, (uint32_t)((int64_t)mrows * p.k * 2));  // A_HANDOFF
   uint4 gv[kStageUnroll], uv[kStageUnroll];
@@ -323,11 +311,6 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
         if (AM == A_SILU_PACKED)
           w = make_uint4(silu_mul2(w.x, uv[u].x), silu_mul2(w.y, uv[u].y), silu_mul2(w.z, uv[u].z),
                          silu_mul2(w.w, uv[u].w));
-        if (GROUPED && (r & 1)) {  // k = 8..15 of the row: these meet the 16x-biased high nibbles
-          const f16x2 q = (f16x2){(f16)0.0625f, (f16)0.0625f};
-          w = make_uint4(as_u32(as_h2(w.x) * q), as_u32(as_h2(w.y) * q), as_u32(as_h2(w.z) * q),
-                         as_u32(as_h2(w.w) * q));
-        }
         const int fg = ((r >> 2) * 4 + ((r & 3) >> 1) * 2) * mrows + mm;  // fragment (kp, g = 2 prow)
         uint2* dst = reinterpret_cast<uint2*>(afr + fg) + (r & 1);
         dst[0] = make_uint2(w.x, w.y);          // halves 0..3 -> g = 2 prow
@@ -346,11 +329,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
 #pragma unroll
     for (int d = 0; d < kSteps; ++d) {
       const u32x4* src = reinterpret_cast<const u32x4*>(bsrc + (int64_t)(kpf + d) * 2 * row_words);
-#if LB_STREAM_LOADS
-      w[d] = __builtin_nontemporal_load(src);
-#else
       w[d] = *src;
-#endif
     }
     if (GROUPED) scl = *reinterpret_cast<const u32x4*>(ssrc + (int64_t)(kpf >> 2) * p.n);
   };
@@ -377,24 +356,6 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   if (tid == 0) afr[n_frag] = (u32x4){0, 0, 0, 0};
   lds_barrier();  // LDS only: the weight ring stays in flight
 
-  // Bias correction.  The MFMA sees 1024 + q against x (k = 0..7 of a row) and
-  // 1024 + 16q against x/16 (k = 8..15), i.e. x*q + 1024x and x~*q + 64x~ with
-  // x~ = 16 * fp16(x/16); subtracting 1032*sum(x) + 72*sum(x~) = 1032*lo + 1152*hi
-  // (sums of the staged values) leaves sum(x * (q - 8)).  Fixed-order sums.
-  for (int t = tid; GROUPED && t < ngw * kMaxM; t += kThreads) {
-    const int gi = t / kMaxM, mm = t - gi * kMaxM;
-    float lo = 0.f, hi = 0.f;
-    if (mm < mrows) {
-      for (int e = 0; e < 4 * kSteps; ++e) {  // the group's 4 k-steps x 4 fragments
-        const u32x4 f = afr[(gi * 4 * kSteps + e) * mrows + mm];
-        lo += (float)as_h2(f[0])[0] + (float)as_h2(f[0])[1] + (float)as_h2(f[1])[0] + (float)as_h2(f[1])[1];
-        hi += (float)as_h2(f[2])[0] + (float)as_h2(f[2])[1] + (float)as_h2(f[3])[0] + (float)as_h2(f[3])[1];
-      }
-    }
-    corr[t] = -(1032.f * lo + 1152.f * hi);
-  }
-  lds_barrier();  // LDS only: the weight ring stays in flight
-
   // A fragment address: rows >= M read the zero entry.
   const bool a_live = mrow < mrows;
   const int a_step = a_live ? 4 * mrows : 0;
@@ -405,13 +366,19 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
 #pragma unroll
   for (int j = 0; j < 4; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
-  // One batch = one scale group: its MFMAs start from the group's correction
-  // and accumulate the exact products in fp32; the group's scale multiplies
-  // that sum once (per-column scales: the sum is added as is).
+  // One batch = one scale group.  The weights are the reference's fp16
+  // fp16(q - 8) * s (marlin_cuda_kernel.cu:131-159: exact q - 8 from one
+  // v_and_or_b32 and one packed add or fma, then one packed multiply by the
+  // group's scale), so every product with an fp16 activation is exact in the
+  // fp32 MFMA accumulation, as in the reference's MMA.  Per-column scales: the
+  // exact q - 8, scaled after the fp16 rounding of the sum.
   auto consume = [&](const u32x4(&w)[kSteps], const u32x4& scl, int batch) {
-    const f32x4 cinit =
-        GROUPED ? *reinterpret_cast<const f32x4*>(corr + (gw0 + batch) * kMaxM + crow0) : (f32x4){0.f, 0.f, 0.f, 0.f};
-    f32x4 grp[4];
+    f16x2 sc2[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {  // column 16j + 8h + c
+      const f16 s = __builtin_bit_cast(f16, (uint16_t)(scl[j] >> (16 * hsel)));
+      sc2[j] = (f16x2){s, s};
+    }
 #pragma unroll
     for (int d = 0; d < kSteps; ++d) {
       const u32x4 t = afr[a_base + (batch * kSteps + d) * a_step];
@@ -422,24 +389,16 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
         const uint32_t partner = (uint32_t)__builtin_amdgcn_mov_dpp((int)own[j], 0x128, 0xf, 0xf, false);  // row_ror:8
         const uint32_t v0 = __builtin_amdgcn_perm(own[j], partner, psel);
         const uint32_t v1 = v0 >> 8;
-        // grouped: biased values (the group's correction removes the bias);
-        // per-column: the exact fp16 (q - 8), accumulated as the reference does
-        const f16x8 bfrag =
-            GROUPED ? __builtin_bit_cast(f16x8, make_uint4(as_u32(nib_lo_biased(v0, nk)), as_u32(nib_lo_biased(v1, nk)),
-                                                           as_u32(nib_hi_biased(v0, nk)), as_u32(nib_hi_biased(v1, nk))))
-                    : __builtin_bit_cast(f16x8, make_uint4(as_u32(nib_lo_to_h2(v0, nk)), as_u32(nib_lo_to_h2(v1, nk)),
-                                                           as_u32(nib_hi_to_h2(v0, nk)), as_u32(nib_hi_to_h2(v1, nk))));
-        grp[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, d == 0 ? cinit : grp[j], 0, 0, 0);
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      if (GROUPED) {
-        const float sc = h2f((uint16_t)(scl[j] >> (16 * hsel)));  // column 16j + 8h + c
-#pragma unroll
-        for (int i = 0; i < 4; ++i) acc[j][i] += grp[j][i] * sc;
-      } else {
-        acc[j] += grp[j];
+        f16x2 l0 = nib_lo_to_h2(v0, nk), l1 = nib_lo_to_h2(v1, nk);
+        f16x2 h0 = nib_hi_to_h2(v0, nk), h1 = nib_hi_to_h2(v1, nk);
+        if (GROUPED) {
+          l0 *= sc2[j];
+          l1 *= sc2[j];
+          h0 *= sc2[j];
+          h1 *= sc2[j];
+        }
+        const f16x8 bfrag = __builtin_bit_cast(f16x8, make_uint4(as_u32(l0), as_u32(l1), as_u32(h0), as_u32(h1)));
+        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, acc[j], 0, 0, 0);
       }
     }
   };

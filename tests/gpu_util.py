@@ -32,22 +32,26 @@ def assert_close_f16(got: np.ndarray, ref: np.ndarray, atol: float = ATOL, rtol:
     return float((g == r).mean())
 
 
-def assert_exact_scale(got: np.ndarray, ref: np.ndarray, exact: np.ndarray, what: str = ""):
-    """Grouped scales: the kernel multiplies each group's fp32 sum of x*(q-8) by
-    the scale once, where the reference rounds every fp16 (q-8)*s product before
-    accumulating.  Against the float64 value of the same sum (``exact``), the
-    kernel must be at least as accurate as the reference is (RMS), and no
-    element may be off by more than one fp16 step plus twice the reference's
-    own RMS rounding noise."""
-    g = np.asarray(got, dtype=np.float64)
-    r = np.asarray(ref, dtype=np.float64)
-    e = np.asarray(exact, dtype=np.float64)
-    rms_got = float(np.sqrt(np.mean((g - e) ** 2)))
-    rms_ref = float(np.sqrt(np.mean((r - e) ** 2)))
-    assert rms_got <= rms_ref + 1e-12, f"{what}: rms error vs exact {rms_got:.3e} > reference's {rms_ref:.3e}"
-    step = np.spacing(np.abs(np.asarray(exact, dtype=np.float16))).astype(np.float64)
-    bad = np.abs(g - e) > step + 2.0 * rms_ref
-    assert not bad.any(), f"{what}: {int(bad.sum())} outputs off the exact value by more than 1 step + 2 rms"
+def assert_reference_rounding(got: np.ndarray, ref: np.ndarray, x: np.ndarray, qweight: np.ndarray,
+                              scales: np.ndarray, group: int, what: str = ""):
+    """Kernels that round every weight as the reference does (fp16 (q - 8) * s,
+    then fp32 accumulation) differ from the oracle's float64-accumulated sum
+    only by fp32 summation order: every output within one fp16 step plus the
+    fp32 summation bound 2^-20 * sum_k |x_k w_k| (about sqrt(K) roundings of
+    the partial sums), and at least 90 % of them equal."""
+    import torch
+
+    from oracle import torch_cpu as T  # equals lowbit_oracle.marlin_dequant_f16 bit for bit (test_oracle_golden)
+
+    w = T.marlin_dequant(torch.from_numpy(np.ascontiguousarray(qweight)),
+                         torch.from_numpy(np.ascontiguousarray(scales)), group).abs().to(torch.float64)
+    bound = (torch.from_numpy(np.abs(np.asarray(x, dtype=np.float64))) @ w).numpy() * 2.0 ** -20
+    g = np.asarray(got).astype(np.float64)
+    r = np.asarray(ref).astype(np.float64)
+    step = np.spacing(np.abs(np.asarray(ref, dtype=np.float16))).astype(np.float64)
+    bad = np.abs(g - r) > step + bound
+    assert not bad.any(), f"{what}: {int(bad.sum())} outputs beyond one fp16 step + the fp32 summation bound"
+    assert float((g == r).mean()) >= 0.9, f"{what}: only {float((g == r).mean()):.3f} of outputs equal the oracle"
 
 
 def f16_ulp_distance(got: np.ndarray, ref: np.ndarray) -> np.ndarray:

@@ -12,7 +12,7 @@ import numpy as np
 import pytest
 
 from oracle import lowbit_oracle as O
-from tests.gpu_util import assert_close_f16, assert_exact_scale, print_case, to_dev, to_np
+from tests.gpu_util import assert_close_f16, assert_reference_rounding, print_case, to_dev, to_np
 
 pytestmark = pytest.mark.gpu
 
@@ -94,7 +94,7 @@ def test_skinny_vs_oracle(dev, m, k, n, group):
         assert exact > 0.9
         _assert_per_column_rounding(got, codes, x, sp)
     else:
-        assert_exact_scale(got, ref, O.marlin_gemm_exact(x, qw, sp, group), what=f"m={m} k={k} n={n}")
+        assert_reference_rounding(got, ref, x, qw, sp, group, what=f"m={m} k={k} n={n}")
 
 
 @pytest.mark.parametrize("group", [128, -1])
@@ -112,7 +112,7 @@ def test_wide_decode_vs_oracle(dev, m, k, group):
         assert exact > 0.9
         _assert_per_column_rounding(got, codes, x, sp)
     else:
-        assert_exact_scale(got, ref, O.marlin_gemm_exact(x, qw, sp, group), what=f"wide m={m} k={k}")
+        assert_reference_rounding(got, ref, x, qw, sp, group, what=f"wide m={m} k={k}")
 
 
 @pytest.mark.parametrize("m,k,n,group", [
@@ -136,7 +136,7 @@ def test_wide_decode_leftovers_vs_oracle(dev, m, k, n, group):
         assert exact > 0.9
         _assert_per_column_rounding(got, codes, x, sp)
     else:
-        assert_exact_scale(got, ref, O.marlin_gemm_exact(x, qw, sp, group), what=f"wide-left m={m} k={k} n={n}")
+        assert_reference_rounding(got, ref, x, qw, sp, group, what=f"wide-left m={m} k={k} n={n}")
     # repeated launches are bit-identical (split partials are summed in split order)
     again = _run_gemm(dev, x, qw, sp, group)
     assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
@@ -169,8 +169,8 @@ def test_gemm_vs_oracle(dev, m):
     got = _run_gemm(dev, x, qw, sp, 128)
     ref = O.marlin_gemm(x, qw, sp, 128)
     exact = assert_close_f16(got, ref, what=f"m={m}")
-    if m <= 16:  # decode kernel: each group's fp32 sum is scaled once
-        assert_exact_scale(got, ref, O.marlin_gemm_exact(x, qw, sp, 128), what=f"m={m}")
+    if m <= 16:  # decode kernel
+        assert_reference_rounding(got, ref, x, qw, sp, 128, what=f"m={m}")
     else:  # prefill kernel: the reference's fp16 (q - 8) * s weights
         assert exact > 0.95
 
@@ -185,7 +185,7 @@ def test_decode_shape_cfg2(dev, m):
     ref = O.marlin_gemm(x, qw, sp, 128)
     exact = assert_close_f16(got, ref, what=f"cfg2 m={m}")
     if m <= 16:  # decode kernel
-        assert_exact_scale(got, ref, O.marlin_gemm_exact(x, qw, sp, 128), what=f"cfg2 m={m}")
+        assert_reference_rounding(got, ref, x, qw, sp, 128, what=f"cfg2 m={m}")
     else:  # prefill kernel, the reference's rounding
         assert exact > 0.95
 
@@ -212,7 +212,7 @@ def test_narrow_decode_vs_oracle(dev, m, k, n, group):
         assert exact > 0.9
         _assert_per_column_rounding(got, codes, x, sp)
     else:
-        assert_exact_scale(got, ref, O.marlin_gemm_exact(x, qw, sp, group), what=f"narrow m={m} k={k} n={n}")
+        assert_reference_rounding(got, ref, x, qw, sp, group, what=f"narrow m={m} k={k} n={n}")
     again = _run_gemm(dev, x, qw, sp, group)
     assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
 

@@ -122,8 +122,8 @@ def test_fused_mlp_model_shape_one_launch(dev, batch):
     launches = capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128, capi.MLP_ONE_LAUNCH)
     print_case("mlp_fused_model", batch, "launches", launches)
     assert launches == 1
-    # auto: the two launches at batch 1, one launch from batch 2 on
-    assert capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128) == (2 if batch == 1 else 1)
+    # auto: always the two launches (the one launch is opt-in)
+    assert capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128) == 2
     args = _problem_dev(HIDDEN, INTER, batch, 7 + batch, dev)
     got = _fused(dev, *args, HIDDEN, INTER, 128, 128)
     ref, _ = _two_launches(dev, *args, HIDDEN, INTER, 128, 128)
@@ -176,3 +176,72 @@ def test_torch_op_matches_reference_op_sequence(dev, batch):
     assert_close_f16(got, to_np(ref_out), what="op vs reference op sequence")
     with pytest.raises(RuntimeError, match="workspace must hold"):
         lc.lowbit_marlin_mlp_fused_out(gu_q, gu_s, d_q, d_s, x, out, ws[:8], HIDDEN, INTER, 128, 128)
+
+
+def _sample_cols(n, count, seed):
+    """`count` 64-column chunks of an N-column Marlin tensor (the layout slices
+    at 64 columns: qweight[:, 2 n0 : 2 n1], scales[:, n0 : n1])."""
+    rng = np.random.default_rng(seed)
+    chunks = np.sort(rng.choice(n // 64, size=count, replace=False))
+    return [(64 * c, 64 * c + 64) for c in chunks]
+
+
+@pytest.mark.parametrize("batch", [1, 4, 16])
+def test_fused_mlp_model_shape_vs_oracle(dev, batch):
+    """The one-launch MLP at the model's shape (hidden 5120, intermediate
+    17408, g128) against the oracle, column-sampled: the gate_up stage on 16
+    chunks of its 34816 columns, the SiLU-gated down stage on 16 chunks of its
+    5120 outputs over the whole [g | u] row; and bit-equal to the two launches."""
+    from neurova_amd import capi
+
+    print_case("mlp_fused_model_oracle", batch)
+    rng = np.random.default_rng(900 + batch)
+    gu_q = rng.integers(-2**31, 2**31, size=(HIDDEN // 16, 4 * INTER), dtype=np.int64).astype(np.int32)
+    d_q = rng.integers(-2**31, 2**31, size=(INTER // 16, 2 * HIDDEN), dtype=np.int64).astype(np.int32)
+    gu_s = (np.abs(rng.normal(0, 0.01, (HIDDEN // 128, 2 * INTER))) + 1e-3).astype(np.float16)
+    d_s = (np.abs(rng.normal(0, 0.01, (INTER // 128, HIDDEN))) + 1e-3).astype(np.float16)
+    x = rng.normal(0, 1, (batch, HIDDEN)).astype(np.float16)
+    args = [to_dev(a, dev) for a in (x, gu_q, gu_s, d_q, d_s)]
+    got = _fused(dev, *args, HIDDEN, INTER, 128, 128, mode=capi.MLP_ONE_LAUNCH)
+    two, mixed = _two_launches(dev, *args, HIDDEN, INTER, 128, 128)
+    assert np.array_equal(got.view(np.uint16), two.view(np.uint16))
+    for n0, n1 in _sample_cols(2 * INTER, 16, batch):
+        assert_close_f16(mixed[:, n0:n1], O.marlin_gemm(x, gu_q[:, 2 * n0:2 * n1], gu_s[:, n0:n1], 128),
+                         what=f"gate_up cols {n0}:{n1}")
+    for n0, n1 in _sample_cols(HIDDEN, 16, batch + 1):
+        assert_close_f16(got[:, n0:n1],
+                         O.marlin_gemm_silu_packed(mixed, d_q[:, 2 * n0:2 * n1], d_s[:, n0:n1], INTER, 128),
+                         what=f"down(silu) cols {n0}:{n1}")
+
+
+def test_fused_mlp_give_up_is_reported_and_recovers(dev):
+    """A one-launch wait that gives up (forced from the host with a spin limit
+    of one poll; every kernel still ends normally) is reported by
+    lb_marlin_mlp_fused_check and by the torch op's check=True, the workspace
+    is zeroed, and the next call is exact again."""
+    import torch
+    import langburst_cuda as lc
+    from neurova_amd import capi
+
+    batch = 4
+    print_case("mlp_fused_give_up", batch)
+    x, gu_q, gu_s, d_q, d_s = _problem_dev(HIDDEN, INTER, batch, 77, dev)
+    two, _ = _two_launches(dev, x, gu_q, gu_s, d_q, d_s, HIDDEN, INTER, 128, 128)
+    ws = torch.zeros((capi.marlin_mlp_fused_workspace_len(batch, HIDDEN, INTER),), dtype=torch.int32, device=dev)
+    scratch = torch.empty((capi.marlin_mlp_fused_scratch_bytes(batch, HIDDEN, INTER),), dtype=torch.uint8, device=dev)
+    out = torch.empty((batch, HIDDEN), dtype=torch.float16, device=dev)
+    try:
+        capi.marlin_mlp_fused_set_spin_limit(1)
+        assert capi.marlin_mlp_fused(x, gu_q, gu_s, d_q, d_s, out, HIDDEN, INTER, 128, 128, ws, scratch,
+                                     mode=capi.MLP_ONE_LAUNCH) == 0
+        assert capi.marlin_mlp_fused_check(ws) == capi.LB_ERR_HANDOFF
+        assert int(ws.abs().sum()) == 0
+        with pytest.raises(RuntimeError, match="gave up waiting"):
+            lc.lowbit_marlin_mlp_fused_out(gu_q, gu_s, d_q, d_s, x, out, ws, HIDDEN, INTER, 128, 128, mode=1,
+                                           check=True)
+        assert int(ws.abs().sum()) == 0
+    finally:
+        capi.marlin_mlp_fused_set_spin_limit(0)
+    lc.lowbit_marlin_mlp_fused_out(gu_q, gu_s, d_q, d_s, x, out, ws, HIDDEN, INTER, 128, 128, mode=1, check=True)
+    assert np.array_equal(to_np(out).view(np.uint16), two.view(np.uint16))
+    assert capi.marlin_mlp_fused_check(ws) == 0 and int(ws.abs().sum()) == 0

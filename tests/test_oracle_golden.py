@@ -317,3 +317,44 @@ def test_byte_formulas():
     assert O.rowwise_bytes(1, 4096, 4096, 4, 128) == 8_667_136
     assert O.rowwise_bytes(1, 17408, 5120, 3, 128) == 34_861_056
     assert O.rowwise_bytes(1, 17408, 5120, 8, 64) == 91_959_296
+
+
+# ---- the vectorised torch-CPU restatement timed as the CPU baseline ----
+
+@pytest.mark.parametrize("bits,group,cols", [(4, 128, 4096), (2, 64, 513), (3, 128, 257), (8, 32, 300)])
+def test_torch_cpu_rowwise_matches_oracle(bits, group, cols):
+    """oracle/torch_cpu.py's dense fp16 matrix is the numpy oracle's fp32
+    ``q * s`` rounded to fp16, bit for bit (``loader.py:442-452``); its GEMV is
+    within the parity tolerance of the oracle's fp32-accumulated one."""
+    import torch
+
+    from oracle import torch_cpu as T
+
+    rows = 64
+    _, packed, scales, x = O.make_rowwise_inputs(rows, cols, bits, group, seed=bits + cols)
+    dense = T.rowwise_dequant_rows(torch.from_numpy(packed), torch.from_numpy(scales), cols, group, bits)
+    want = O.rowwise_dequant_f32(packed, scales, cols, group, bits).astype(np.float16)
+    assert np.array_equal(dense.numpy().view(np.uint16), want.view(np.uint16))
+    y = T.rowwise_gemv(torch.from_numpy(packed), torch.from_numpy(scales), torch.from_numpy(x[0]), cols, group, bits)
+    ref = O.rowwise_gemv(packed, scales, x[0], cols, group, bits).astype(np.float64)
+    assert np.all(np.abs(y.numpy().astype(np.float64) - ref) <= 1e-2 + 1e-3 * np.abs(ref) + 2e-3 * np.abs(ref).max())
+
+
+@pytest.mark.parametrize("group", [128, -1])
+def test_torch_cpu_marlin_matches_oracle(group):
+    """The torch-CPU Marlin unpack and fp16 dequant equal the oracle's bit for
+    bit; the product is within the parity tolerance."""
+    import torch
+
+    from oracle import torch_cpu as T
+
+    m, k, n = 3, 512, 768
+    _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128 if group == 128 else -1, seed=31)
+    if group == -1:
+        s = (np.abs(np.random.default_rng(2).normal(0, 0.01, (1, n))) + 1e-3).astype(np.float16)
+        sp = O.marlin_pack_scales(s, per_column=True)
+    w = T.marlin_dequant(torch.from_numpy(qw), torch.from_numpy(sp), group)
+    assert np.array_equal(w.numpy().view(np.uint16), O.marlin_dequant_f16(qw, sp, group).view(np.uint16))
+    y = T.marlin_gemm(torch.from_numpy(x), torch.from_numpy(qw), torch.from_numpy(sp), group).numpy()
+    ref = O.marlin_gemm(x, qw, sp, group).astype(np.float64)
+    assert np.all(np.abs(y.astype(np.float64) - ref) <= 1e-2 + 1e-3 * np.abs(ref))

@@ -188,3 +188,54 @@ def test_wrappers_refuse_cpu_execution(tmp_path):
         st.tensor("model.layers.0.mlp.gate_up_proj.weight").gemv(torch.zeros(256, dtype=torch.float16))
     with pytest.raises(RuntimeError, match="no CPU execution path"):
         st.tensor("model.embed_tokens.weight").row_dequant(3)
+
+
+def test_marlin_wrapper_argument_checks(tmp_path, monkeypatch):
+    """LowBitMarlinTensor's reference argument checks (loader.py:337-413) run
+    before any device work; the environment knobs are validated."""
+    import torch
+    from neurova_amd import store
+    from neurova_amd.store import QuantizedStore
+
+    _checkpoint(tmp_path)
+    st = QuantizedStore(tmp_path, device="cpu")
+    down = st.tensor("model.layers.0.mlp.gate_up_proj.weight")
+    k = down.cols
+    with pytest.raises(ValueError, match="expects mixed"):
+        down.gemm_silu_packed(torch.zeros((1, 1, 2 * k), dtype=torch.float16), k)
+    with pytest.raises(ValueError, match="hidden must match"):
+        down.gemm_silu_packed(torch.zeros((1, 2 * k), dtype=torch.float16), k + 128)
+    with pytest.raises(ValueError, match="mixed width must be 2\\*hidden"):
+        down.gemm_silu_packed(torch.zeros((1, 2 * k + 2), dtype=torch.float16), k)
+    with pytest.raises(RuntimeError, match="no CPU execution path"):
+        down.gemm_silu_packed(torch.zeros((2 * k,), dtype=torch.float16), k)
+    with pytest.raises(ValueError, match="expects x"):
+        down.gemm_argmax(torch.zeros((1, 1, k), dtype=torch.float16))
+    with pytest.raises(ValueError, match="expects x"):
+        down.gemm(torch.zeros((k,), dtype=torch.float16))
+    with pytest.raises(RuntimeError, match="does not support row_dequant"):
+        down.row_dequant(0)
+
+    assert store.lowbit_rows_per_cta() == 8 and store.marlin_direct_max_batch() == 256
+    monkeypatch.setenv("LANGBURST_LOWBIT_ROWS_PER_CTA", "16")
+    monkeypatch.setenv("LANGBURST_MARLIN_DIRECT_MAX_BATCH", "4")
+    assert store.lowbit_rows_per_cta() == 16 and store.marlin_direct_max_batch() == 4
+    monkeypatch.setenv("LANGBURST_LOWBIT_ROWS_PER_CTA", "5")
+    with pytest.raises(ValueError, match="rows_per_cta must be one of: 4, 8, 16"):
+        store.lowbit_rows_per_cta()
+    monkeypatch.setenv("LANGBURST_MARLIN_DIRECT_MAX_BATCH", "0")
+    with pytest.raises(ValueError, match=">= 1"):
+        store.marlin_direct_max_batch()
+
+
+@pytest.mark.parametrize("policy,batch,cached", [("off", 1, False), ("", 1, True), ("decode_only", 1, True),
+                                                 ("decode_only", 2, False), ("small", 2, True), ("small", 3, False),
+                                                 ("all", 64, True)])
+def test_output_cache_policy(monkeypatch, policy, batch, cached):
+    """The admission rule of the reference's Marlin output cache (loader.py:29-62); an empty
+    policy string is not one of the "off" spellings there, so it caches."""
+    from neurova_amd.store import _OutputCache
+
+    monkeypatch.setenv("LANGBURST_MARLIN_OUT_CACHE_POLICY", policy)
+    monkeypatch.delenv("LANGBURST_MARLIN_OUT_CACHE_MAX_BATCH", raising=False)
+    assert _OutputCache.wants(batch) is cached
