@@ -36,7 +36,8 @@ enum lb_status {
   LB_ERR_WORKSPACE = 5,  /* workspace shorter than required */
   LB_ERR_SCRATCH = 6,    /* scratch buffer shorter than lb_marlin_scratch_bytes() */
   LB_ERR_HIP = 7,        /* the HIP runtime reported an error at launch */
-  LB_ERR_HANDOFF = 8     /* lb_marlin_mlp_fused_check: an in-kernel wait gave up (output not valid) */
+  LB_ERR_HANDOFF = 8,    /* lb_marlin_mlp_fused_check: an in-kernel wait gave up (output not valid) */
+  LB_ERR_NOALLOC_LIMIT = 9 /* lb_marlin_gemm_noalloc: the problem needs more than its static scratch */
 };
 
 typedef void* lb_stream_t; /* hipStream_t */
@@ -196,6 +197,22 @@ int lb_marlin_mlp_fused_check(int32_t* workspace, int64_t workspace_len, lb_stre
  * 262144; values < 1 restore the default).  Lets a test force the give-up
  * path from the host with every kernel still ending normally. */
 void lb_marlin_mlp_fused_set_spin_limit(int32_t polls);
+
+/* lb_marlin_gemm without caller scratch and without any allocation: no
+ * counterpart in the reference; for callers that cannot allocate (code under
+ * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * The split-K partials go to a static device array of
+ * lb_marlin_noalloc_scratch_limit() bytes (32 MiB) that each GPU holds until
+ * the process ends; problems whose plan needs more return
+ * LB_ERR_NOALLOC_LIMIT before anything is launched (every decode shape up to
+ * M = 64 of the BASELINE projections fits; M = 2048 prefill does not).  All
+ * calls on one GPU share that array: calls that overlap (other streams) race
+ * and must be serialised by the caller.  Same arguments, workspace contract
+ * and results as lb_marlin_gemm. */
+size_t lb_marlin_noalloc_scratch_limit(void);
+int lb_marlin_gemm_noalloc(const uint16_t* A, const int32_t* B, uint16_t* C, const uint16_t* s,
+                           int64_t prob_m, int64_t prob_n, int64_t prob_k,
+                           int32_t* workspace, int64_t workspace_len, int64_t groupsize, lb_stream_t stream);
 
 /* Dense fp16 W[N, K] = fp16((q - 8) * s) (or q - 8 for per-column scales),
  * bit-exact with the reference's in-kernel dequant (csrc/marlin_cuda_kernel.cu:131-159).

@@ -36,7 +36,7 @@ ROCM = Path(os.environ.get("ROCM_PATH", "/opt/rocm"))
 HIPCC = str(ROCM / "bin" / "hipcc")
 ARCH = "gfx950"
 
-HIP_SOURCES = ["lb_rowwise.hip", "lb_marlin.hip", "lb_probe.hip"]
+HIP_SOURCES = ["lb_rowwise.hip", "lb_marlin.hip", "lb_probe.hip", "lb_noalloc.hip"]
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

@@ -25,6 +25,7 @@ LB_ERR_WORKSPACE = 5
 LB_ERR_SCRATCH = 6
 LB_ERR_HIP = 7
 LB_ERR_HANDOFF = 8
+LB_ERR_NOALLOC_LIMIT = 9
 
 P = ctypes.c_void_p
 I64 = ctypes.c_int64
@@ -46,6 +47,8 @@ _SIGNATURES = {
     "lb_marlin_mlp_streaming": ([P, P, P, P, P, P, P, P, I64, I64, I64, I64, I64, P, SZ, P], ctypes.c_int),
     "lb_marlin_dequant": ([P, P, P, I64, I64, I64, P], ctypes.c_int),
     "lb_probe_stream_read": ([P, SZ, P, I32, P], ctypes.c_int),
+    "lb_marlin_noalloc_scratch_limit": ([], SZ),
+    "lb_marlin_gemm_noalloc": ([P, P, P, P, I64, I64, I64, P, I64, I64, P], ctypes.c_int),
     "lb_marlin_mlp_fused_scratch_bytes": ([I64, I64, I64], SZ),
     "lb_marlin_mlp_fused_workspace_len": ([I64, I64, I64], I64),
     "lb_marlin_mlp_fused_launches": ([I64, I64, I64, I64, I64, I32], ctypes.c_int),
@@ -193,3 +196,14 @@ def marlin_dequant(b, s, w_nk, k, group_size) -> int:
 def probe_stream_read(src, sink, workgroups) -> int:
     return lib().lb_probe_stream_read(_ptr(src), src.numel() * src.element_size(), _ptr(sink), int(workgroups),
                                       _stream(src))
+
+
+def marlin_noalloc_scratch_limit() -> int:
+    return int(lib().lb_marlin_noalloc_scratch_limit())
+
+
+def marlin_gemm_noalloc(a, b, c, s, workspace, group_size) -> int:
+    m, k = a.shape
+    n = b.shape[1] // 2
+    return lib().lb_marlin_gemm_noalloc(_ptr(a), _ptr(b), _ptr(c), _ptr(s), m, n, k, _ptr(workspace),
+                                        workspace.numel(), group_size, _stream(a))

@@ -10,6 +10,7 @@
 #include <mutex>
 
 #include "marlin_gemm.hpp"
+#include "marlin_run.hpp"
 #include "marlin_mlp.hpp"
 #include "marlin_skinny.hpp"
 
@@ -330,8 +331,6 @@ inline int normalize_group(int64_t g, int64_t k, int& grouped) {
   return LB_ERR_PROB_SHAPE;
 }
 
-enum Variant { V_PLAIN = 0, V_SILU = 1, V_ARGMAX = 2 };
-
 int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uint16_t* s, int64_t m, int64_t n,
         int64_t k, int32_t* workspace, int64_t workspace_len, int64_t groupsize, int64_t* argmax_state,
         int64_t* argmax_out, void* scratch, size_t scratch_bytes, hipStream_t st) {
@@ -433,6 +432,7 @@ extern "C" const char* lb_status_string(int status) {
     case LB_ERR_SCRATCH: return "scratch too small";
     case LB_ERR_HIP: return "HIP runtime error";
     case LB_ERR_HANDOFF: return "in-kernel hand-off gave up; output not valid";
+    case LB_ERR_NOALLOC_LIMIT: return "problem needs more than the static no-allocation scratch";
     default: return "unknown status";
   }
 }
