@@ -47,6 +47,9 @@ HIP_FLAGS = [
     # keep hipcc from emitting packed-fp32 (v_pk_*_f32) instructions
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-ffp-contract=fast",
+    # gfx950 preloads the first 16 dwords of scalar kernel arguments into
+    # SGPRs at wave launch: the first loads need no kernarg fetch
+    "-mllvm", "-amdgpu-kernarg-preload-count=16",
 ]
 
 

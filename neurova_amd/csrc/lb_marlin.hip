@@ -366,7 +366,9 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
     p.kp_total = (int)(k / 32); p.n_cg = pl.n_cg;
     dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
 #define LB_SK(AMV, EPV, GV, CV) \
-  hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, EPV, GV, CV>), grid, dim3(skinny::kThreads), pl.lds, st, p)
+  hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, EPV, GV, CV>), grid, dim3(skinny::kThreads), pl.lds, st, \
+                     p.a, p.b, p.s, p.c, p.counters, p.partial, p.m, p.n, p.k, p.splits, p.n_cg, p.tile_keys,     \
+                     p.argmax_state, p.argmax_out)
 #define LB_SKC(AMV, EPV, GV)                              \
   do {                                                    \
     if (pl.cpw == 4) LB_SK(AMV, EPV, GV, 4);              \

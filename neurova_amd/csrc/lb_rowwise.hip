@@ -277,18 +277,69 @@ __device__ __forceinline__ void decode_unit(const uint32_t* w, uint32_t (&b)[16]
   }
 }
 
+// Arguments as scalars, the ones the prologue needs first: gfx950 preloads
+// the leading 16 dwords into SGPRs at wave launch (a struct argument is not
+// preloaded), so the code prefetch below needs no kernarg fetch.
 template <int BITS, int NW, int R, int UPL>
-__global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(Params p) {
+__global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t* q0, const uint8_t* q1,
+                                                                  const uint16_t* s0, const uint16_t* s1,
+                                                                  const uint16_t* x, int packed_cols, int scale_cols,
+                                                                  int cols, int rows, int unit_shift, uint16_t* y0,
+                                                                  uint16_t* y1) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
-  const int units = (int)(p.cols >> 5);
+  const int units = cols >> 5;
   u32x4* xt = reinterpret_cast<u32x4*>(smem);                           // [4][units] pair words
   float* corr = reinterpret_cast<float*>(smem + (size_t)units * 64);    // [units]
   const int tid = threadIdx.x;
   constexpr int z = 1 << (BITS - 1);
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
+
+  // ---- the rows' first kPre lane steps of codes and scales, issued before
+  // the activation staging so that their latency overlaps it ----
+  const int64_t row0 = ((int64_t)blockIdx.x * kLdsWaves + wave) * R;
+  const uint8_t* const qm[2] = {q0, q1};
+  const uint16_t* const sm[2] = {s0, s1};
+  // per-row bases, wave-uniform; 32-bit offsets from them in the loop
+  const uint32_t* qrow[NW][R];
+  const uint16_t* srow[NW][R];
+#pragma unroll
+  for (int a = 0; a < NW; ++a)
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      const int64_t row = row0 + r < rows ? row0 + r : rows - 1;
+      qrow[a][r] = reinterpret_cast<const uint32_t*>(qm[a] + row * packed_cols);
+      srow[a][r] = sm[a] + row * scale_cols;
+    }
+  constexpr int kStepWords = UPL * BITS;
+  // 2 bits: 64 bytes of codes per lane (most of a 17408-column row); wider
+  // codes one step (measured: more registers held across the staging cost
+  // more than the latency they hide)
+  constexpr int kPre = BITS == 2 ? 16 / kStepWords : 1;
+  auto load_step = [&](int u0, uint32_t (&w)[NW][R][kStepWords], float (&sc)[UPL][NW][R])
+      __attribute__((always_inline)) {
+#pragma unroll
+    for (int a = 0; a < NW; ++a)
+#pragma unroll
+      for (int r = 0; r < R; ++r) {
+        const uint32_t* src = qrow[a][r] + (uint32_t)u0 * BITS;
+#pragma unroll
+        for (int d = 0; d < kStepWords; ++d) w[a][r][d] = __builtin_nontemporal_load(src + d);
+#pragma unroll
+        for (int j = 0; j < UPL; ++j) sc[j][a][r] = h2f(srow[a][r][(uint32_t)(u0 + j) >> unit_shift]);
+      }
+  };
+  uint32_t wpre[kPre][NW][R][kStepWords];
+  float spre[kPre][UPL][NW][R];
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    // steps past the row load its last step (in bounds; not used)
+    const int u0 = min(UPL * lane + i * UPL * kWave, units - UPL);
+    load_step(u0, wpre[i], spre[i]);
+  }
 
   // ---- stage the activation row in pair order, and each unit's z * sum(x) ----
   for (int u = tid; u < units; u += kLdsThreads) {
-    const uint4* xs = reinterpret_cast<const uint4*>(p.x + (int64_t)u * 32);
+    const uint4* xs = reinterpret_cast<const uint4*>(x + (int64_t)u * 32);
     uint32_t xd[16];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
@@ -316,19 +367,6 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(Params p) {
   __syncthreads();
 
   // ---- R rows of each of NW matrices per wave ----
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
-  const int64_t row0 = ((int64_t)blockIdx.x * kLdsWaves + wave) * R;
-  // per-row bases, wave-uniform; 32-bit offsets from them in the loop
-  const uint32_t* qrow[NW][R];
-  const uint16_t* srow[NW][R];
-#pragma unroll
-  for (int a = 0; a < NW; ++a)
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      const int64_t row = row0 + r < p.rows ? row0 + r : p.rows - 1;
-      qrow[a][r] = reinterpret_cast<const uint32_t*>(p.q[a] + row * p.packed_cols);
-      srow[a][r] = p.s[a] + row * p.scale_cols;
-    }
   float acc[NW][R];
 #pragma unroll
   for (int a = 0; a < NW; ++a)
@@ -338,19 +376,8 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(Params p) {
   // per step, so each code load is 16 contiguous bytes: wider loads per
   // instruction move the weight stream faster.  A lane adds its units in
   // increasing order.
-  for (int u0 = UPL * lane; u0 < units; u0 += UPL * kWave) {
-    uint32_t w[NW][R][UPL * BITS];
-    float sc[UPL][NW][R];
-#pragma unroll
-    for (int a = 0; a < NW; ++a)
-#pragma unroll
-      for (int r = 0; r < R; ++r) {
-        const uint32_t* src = qrow[a][r] + (uint32_t)u0 * BITS;
-#pragma unroll
-        for (int d = 0; d < UPL * BITS; ++d) w[a][r][d] = __builtin_nontemporal_load(src + d);
-#pragma unroll
-        for (int j = 0; j < UPL; ++j) sc[j][a][r] = h2f(srow[a][r][(uint32_t)(u0 + j) >> p.unit_shift]);
-      }
+  auto step = [&](int u0, const uint32_t (&w)[NW][R][kStepWords], const float (&sc)[UPL][NW][R])
+      __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < UPL; ++j) {
       const int u = u0 + j;
@@ -385,13 +412,25 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(Params p) {
           acc[a][r] = __builtin_fmaf(t, sc[j][a][r], acc[a][r]);  // explicit: one rounding in every instantiation
         }
     }
+  };
+#pragma unroll
+  for (int i = 0; i < kPre; ++i) {
+    const int u0 = UPL * lane + i * UPL * kWave;
+    if (u0 < units) step(u0, wpre[i], spre[i]);
   }
+  for (int u0 = UPL * lane + kPre * UPL * kWave; u0 < units; u0 += UPL * kWave) {
+    uint32_t w[NW][R][kStepWords];
+    float sc[UPL][NW][R];
+    load_step(u0, w, sc);
+    step(u0, w, sc);
+  }
+  uint16_t* const ym[2] = {y0, y1};
 #pragma unroll
   for (int a = 0; a < NW; ++a)
 #pragma unroll
     for (int r = 0; r < R; ++r) {
       const float v = wave_sum(acc[a][r]);
-      if (lane == 0 && row0 + r < p.rows) p.y[a][row0 + r] = f2h(v);
+      if (lane == 0 && row0 + r < rows) ym[a][row0 + r] = f2h(v);
     }
 }
 
@@ -483,7 +522,10 @@ int launch_lds(const Params& p, int bits, hipStream_t st) {
   // mixed (g64 faster, g128 slower); 4 bits 15 % slower, so 3-8 bits keep one.
   const bool pairs = ((p.cols >> 5) & 1) == 0;
   switch (bits) {
-#define LB_LAUNCH(B, U) hipLaunchKernelGGL((rowwise_lds_kernel<B, NW, R, U>), grid, dim3(kLdsThreads), lds, st, p)
+#define LB_LAUNCH(B, U)                                                                                   \
+  hipLaunchKernelGGL((rowwise_lds_kernel<B, NW, R, U>), grid, dim3(kLdsThreads), lds, st, p.q[0], p.q[1], p.s[0], \
+                     p.s[1], p.x, (int)p.packed_cols, (int)p.scale_cols, (int)p.cols, (int)p.rows, p.unit_shift,    \
+                     p.y[0], p.y[1])
 #define LB_LCASE(B)            \
   case B:                      \
     if (pairs) LB_LAUNCH(B, 2); \
@@ -507,7 +549,8 @@ int launch(Params p, int nw, int bits, hipStream_t st) {
   const int64_t gu = p.group / 32;  // units per group
   const bool lds = fast && p.batch == 1 && p.cols % 32 == 0 && (bits == 2 || bits == 3 || bits == 4 || bits == 8) &&
                    (p.cols >> 5) * kLdsUnitBytes <= kLdsMaxBytes && (gu & (gu - 1)) == 0 &&
-                   p.packed_cols * (p.rows > 0 ? 1 : 0) <= (int64_t)0xffffffff / 2;
+                   p.packed_cols * (p.rows > 0 ? 1 : 0) <= (int64_t)0xffffffff / 2 &&
+                   p.rows < (int64_t(1) << 31) && p.scale_cols < (int64_t(1) << 31);  // int kernel arguments
   if (lds) {
     p.unit_shift = 0;
     while ((int64_t(1) << p.unit_shift) < gu) ++p.unit_shift;

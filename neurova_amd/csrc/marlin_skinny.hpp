@@ -573,8 +573,20 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   return true;
 }
 
+// The arguments the prologue needs come first, as separate scalars: gfx950
+// preloads the leading kernel arguments into SGPRs at wave launch (the build
+// asks for 16 dwords), so the first weight loads do not wait for a kernarg
+// fetch.  A struct argument is not preloaded.
 template <int AM, int EPI, bool GROUPED, int CPW>
-__global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(Params p) {
+__global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(const uint16_t* a, const uint32_t* b,
+                                                                 const uint16_t* s, uint16_t* c, int32_t* counters,
+                                                                 float* partial, int m, int n, int k, int splits,
+                                                                 int n_cg, uint64_t* tile_keys, int64_t* argmax_state,
+                                                                 int64_t* argmax_out) {
+  Params p{};
+  p.a = a; p.b = b; p.s = s; p.c = c; p.counters = counters; p.partial = partial;
+  p.m = m; p.n = n; p.k = k; p.splits = splits; p.kp_total = k >> 5; p.n_cg = n_cg;
+  p.tile_keys = tile_keys; p.argmax_state = argmax_state; p.argmax_out = argmax_out;
   skinny_tile<AM, EPI, GROUPED, CPW>(p, blockIdx.x, blockIdx.y);
 }
 
