@@ -158,6 +158,8 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 
 struct Plan {
   bool skinny = true;
+  bool direct = false; // decode kernel with A fragments loaded per step (skinny::A_DIRECT)
+  int mr = 1;          // decode: 16-row blocks of the MFMA tile
   int mb = 1;        // GEMM: 16-row blocks per workgroup
   int n_mb = 1;
   int n_cg = 0;      // column tiles (decode: 64 * cpw columns; GEMM: 256)
@@ -171,6 +173,7 @@ struct Plan {
   size_t x_bytes = 0; // decode kernel: staged activations
   size_t partial_bytes = 0;
   size_t keys_bytes = 0;
+  size_t act_bytes = 0;  // A_DIRECT with SiLU-gated A: fp16(silu(g) * u) [M][K], after the partials
 };
 
 constexpr int kSkinnyWGsPerCU = 2;  // decode workgroups resident per CU (register-limited)
@@ -212,8 +215,9 @@ inline int choose_tail_splits(int64_t tail, int64_t slots, int groups) {
 
 // Decode tiling with `cpw` chunks per workgroup: the k split count, or 0
 // when the tiling cannot run (some wave would get no scale group, or the
-// A slice does not fit LDS without the workspace to split K).
-inline int skinny_splits(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int cpw) {
+// staged A slice does not fit LDS without the workspace to split K).
+// `direct`: A is not staged (skinny::A_DIRECT), so LDS sets no bound.
+inline int skinny_splits(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int cpw, bool direct = false) {
   const int n_cg = (int)(n / (64 * cpw));
   const int ksub = skinny::kWaves / cpw;
   const int groups = (int)(k / 128);
@@ -229,48 +233,104 @@ inline int skinny_splits(int64_t m, int64_t n, int64_t k, int64_t workspace_len,
   const int s_traffic = (int)std::max<int64_t>(1, k / (32 * m));
   if (s > s_traffic) s = s_traffic;
   // the decode kernel stages its whole A slice in LDS
-  const int s_lds = (int)((x_all + kSkinnyMaxX - 1) / kSkinnyMaxX);
+  const int s_lds = direct ? 1 : (int)((x_all + kSkinnyMaxX - 1) / kSkinnyMaxX);
   if (s < s_lds) s = s_lds;
   if (s > groups / ksub) s = groups / ksub;  // every wave at least one group
   if (s > 256) s = 256;  // the kernel's split arithmetic is 32-bit: groups * S < 2^32
   if (s < 1) s = 1;
   if (!can_split) s = 1;
   if (groups / s < ksub) return 0;
-  if ((size_t)((groups + s - 1) / s) * 128 * (size_t)m * 2 > kSkinnyMaxX) return 0;
+  if (!direct && (size_t)((groups + s - 1) / s) * 128 * (size_t)m * 2 > kSkinnyMaxX) return 0;
   return s;
 }
 
-// `am`: the A mode of the launch (gemm::A_PLAIN or gemm::A_SILU_PACKED).
-inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am) {
+// Decode tilings (M <= 16 staged, M <= 32 direct): the chunks per workgroup
+// and the k split count, or cpw = 0 when none runs.
+struct Tiling {
+  int cpw = 0, s = 0;
+};
+
+// Staged A (M <= 16): 4 chunks (one per wave) per workgroup, unless the
+// narrow N then needs more than kSkinnyMaxSplits k splits to fill the chip:
+// then 2 or 1 chunks, whose waves share the workgroup's k range.
+inline Tiling staged_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
+  Tiling t;
+  for (int c = skinny::kWaves; c >= 1; c /= 2) {
+    const int sc = skinny_splits(m, n, k, workspace_len, c);
+    if (sc == 0) continue;
+    if (t.cpw == 0 || sc < t.s) {
+      t.cpw = c;
+      t.s = sc;
+    }
+    if (t.s <= kSkinnyMaxSplits) break;
+  }
+  return t;
+}
+
+// Direct A: every workgroup reads its A fragments itself, so the split cap
+// S * M <= K / 32 bites early at larger M; the widest tiling that gives 1.5
+// workgroups per CU within kSkinnyMaxSplits splits, else the one with the
+// most workgroups.
+inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
+  Tiling t;
+  int64_t most = -1;
+  for (int c = skinny::kWaves; c >= 1; c /= 2) {
+    const int sc = skinny_splits(m, n, k, workspace_len, c, true);
+    if (sc == 0) continue;
+    const int64_t w = (n / (64 * c)) * sc;
+    if (sc <= kSkinnyMaxSplits && 2 * w >= 3 * (int64_t)device_cus()) return Tiling{c, sc};
+    if (w > most) {
+      most = w;
+      t = Tiling{c, sc};
+    }
+  }
+  return t;
+}
+
+// `am`: the A mode of the launch (gemm::A_PLAIN or gemm::A_SILU_PACKED);
+// `argmax`: the fused-argmax variant; `allow_direct`: false plans only the
+// staged decode tiles (the one-launch MLP's phases).
+//
+// Which decode form (measured on the BASELINE decode shapes): the direct
+// form where the tiles are narrow (the waves of a workgroup then share
+// little A, and staging the whole slice before the loop holds them up), or
+// where LDS forces the staged form to more splits than one wave of resident
+// workgroups; the staged form where 4-chunk tiles share the slice.  The
+// SiLU-gated direct form first forms fp16(silu(g) * u) in a launch of its
+// own, which does not pay below 5 rows.  M = 17..32: the direct form on
+// 64-column tiles only; wider tiles go to the prefill kernel.
+inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am, bool argmax = false,
+                      bool allow_direct = true) {
   Plan pl;
   pl.n_cg = (int)(n / 256);
   const int groups = (int)(k / 128);
-  // Decode: 4 chunks (one per wave) per workgroup, unless the narrow N then
-  // needs more than kSkinnyMaxSplits k splits to fill the chip: then 2 or 1
-  // chunks, whose waves share the workgroup's k range.
-  int cpw = 0, s = 0;
-  constexpr int kCpwWidest = 4, kCpwNarrowest = 1;
-  if (m <= skinny::kMaxM) {
-    for (int c = kCpwWidest; c >= kCpwNarrowest; c /= 2) {
-      const int sc = skinny_splits(m, n, k, workspace_len, c);
-      if (sc == 0) continue;
-      if (cpw == 0 || sc < s) {
-        cpw = c;
-        s = sc;
-      }
-      if (s <= kSkinnyMaxSplits) break;
-    }
+  const Tiling ts = m <= skinny::kMaxM ? staged_tiling(m, n, k, workspace_len) : Tiling{};
+  const Tiling td = (allow_direct && !argmax && m <= 16 * skinny::kMaxMR) ? direct_tiling(m, n, k, workspace_len)
+                                                                         : Tiling{};
+  bool direct = false;
+  if (td.cpw > 0) {
+    if (m > skinny::kMaxM) direct = td.cpw == 1;
+    else if (ts.cpw == 0) direct = true;
+    else if (am == gemm::A_SILU_PACKED && m <= 4) direct = false;
+    else direct = td.cpw <= 2 || (ts.cpw == td.cpw && ts.s > td.s);
   }
+  const Tiling tl = direct ? td : ts;
+  const int cpw = tl.cpw, s = tl.s;
   if (cpw > 0) {
     pl.skinny = true;
+    pl.direct = direct;
+    pl.mr = direct ? (int)((m + 15) / 16) : 1;
     pl.cpw = cpw;
     pl.n_cg = (int)(n / (64 * cpw));
     pl.splits = s;
     const int max_groups = (groups + s - 1) / s;
-    pl.x_bytes = (size_t)max_groups * 128 * (size_t)m * 2;  // staged A slice (at most kSkinnyMaxX)
-    const size_t stage = pl.x_bytes + 16;                    // + the zero entry
-    pl.lds = std::max(stage, (size_t)m * skinny::kCols * 4);
+    pl.x_bytes = direct ? 0 : (size_t)max_groups * 128 * (size_t)m * 2;  // staged A slice (at most kSkinnyMaxX)
+    const size_t stage = direct ? 0 : pl.x_bytes + 16;                   // + the zero entry
+    // the epilogue's fp32 tile [M][256] (direct plans on wide tiles store per wave)
+    const size_t tile = (direct && cpw == skinny::kWaves) ? 0 : (size_t)m * skinny::kCols * 4;
+    pl.lds = std::max(stage, tile);
     pl.partial_bytes = pl.splits > 1 ? align_up((size_t)pl.splits * (size_t)m * (size_t)n * 4) : 0;
+    if (direct && am == gemm::A_SILU_PACKED) pl.act_bytes = align_up((size_t)m * (size_t)k * 2);
   } else {
     pl.skinny = false;
     // 128-row tiles (two workgroups per CU) where M fills them; the SiLU-gated
@@ -347,15 +407,51 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   // The GEMM kernel addresses A, B and s through 32-bit buffer resources.
   const int64_t a_bytes = m * k * 2 * (var == V_SILU ? 2 : 1);
   if (m > skinny::kMaxM && (a_bytes >= (1LL << 31) || k * n / 2 >= (1LL << 31))) return LB_ERR_PROB_SHAPE;
-  const Plan pl = make_plan(m, n, k, workspace_len, var == V_SILU ? gemm::A_SILU_PACKED : gemm::A_PLAIN);
+  const Plan pl = make_plan(m, n, k, workspace_len, var == V_SILU ? gemm::A_SILU_PACKED : gemm::A_PLAIN,
+                            var == V_ARGMAX);
   if (workspace_len < counters_needed(pl, var == V_ARGMAX)) return LB_ERR_WORKSPACE;
-  const size_t need = pl.partial_bytes + (var == V_ARGMAX ? pl.keys_bytes : 0);
+  const size_t need = pl.partial_bytes + (var == V_ARGMAX ? pl.keys_bytes : 0) + pl.act_bytes;
   if (need > 0 && (!scratch || scratch_bytes < need)) return LB_ERR_SCRATCH;
   if (need > 0 && !lbh::aligned(scratch, 16)) return LB_ERR_ALIGN;
 
   unsigned char* sc = reinterpret_cast<unsigned char*>(scratch);
   float* partial = pl.partial_bytes ? reinterpret_cast<float*>(sc) : nullptr;
   uint64_t* keys = var == V_ARGMAX ? reinterpret_cast<uint64_t*>(sc + pl.partial_bytes) : nullptr;
+
+  if (pl.direct) {
+    // A fragments loaded per step; the SiLU-gated A is formed once into
+    // scratch first (the staged variant forms it in every tile).
+    const uint16_t* av = a;
+    if (var == V_SILU) {
+      uint16_t* act = reinterpret_cast<uint16_t*>(sc + pl.partial_bytes);
+      const int64_t items = m * (k / 8);
+      hipLaunchKernelGGL(skinny::silu_pack_kernel, dim3((unsigned)((items + 255) / 256)), dim3(256), 0, st, a, act,
+                         (int)m, (int)k);
+      av = act;
+    }
+    const int32_t sp = pl.splits, ncg = pl.n_cg;
+    dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
+#define LB_SKD(GV, CV, MRV)                                                                                       \
+  hipLaunchKernelGGL((skinny::marlin_skinny_kernel<skinny::A_DIRECT, skinny::EPI_STORE, GV, CV, MRV>), grid,     \
+                     dim3(skinny::kThreads), pl.lds, st, av, reinterpret_cast<const uint32_t*>(b), s, c, workspace, \
+                     partial, (int)m, (int)n, (int)k, sp, ncg, nullptr, nullptr, nullptr)
+#define LB_SKDC(GV, MRV)                          \
+  do {                                            \
+    if (pl.cpw == 4) LB_SKD(GV, 4, MRV);          \
+    else if (pl.cpw == 2) LB_SKD(GV, 2, MRV);     \
+    else LB_SKD(GV, 1, MRV);                      \
+  } while (0)
+    if (pl.mr == 1) {
+      if (grouped) LB_SKDC(true, 1);
+      else LB_SKDC(false, 1);
+    } else {  // M = 17..32: 64-column tiles only (make_plan)
+      if (grouped) LB_SKD(true, 1, 2);
+      else LB_SKD(false, 1, 2);
+    }
+#undef LB_SKDC
+#undef LB_SKD
+    return lbh::launch_status();
+  }
 
   if (pl.skinny) {
     skinny::Params p{};
@@ -448,7 +544,9 @@ extern "C" size_t lb_marlin_scratch_bytes(int64_t prob_m, int64_t prob_n, int64_
   // Largest over the variants (the SiLU-gated one may use other tiles).
   const marlin::Plan a = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN);
   const marlin::Plan b = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_SILU_PACKED);
-  return std::max(a.partial_bytes + a.keys_bytes, b.partial_bytes + b.keys_bytes);
+  const marlin::Plan c = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN, true);
+  return std::max(std::max(a.partial_bytes + a.keys_bytes, b.partial_bytes + b.keys_bytes + b.act_bytes),
+                  c.partial_bytes + c.keys_bytes);
 }
 
 extern "C" int lb_marlin_gemm(const uint16_t* A, const int32_t* B, uint16_t* C, const uint16_t* s,
@@ -624,10 +722,19 @@ std::atomic<int> g_mlp_spin_limit{mlp::kSpinLimit};
 FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g1, bool g2, int mode,
                             bool occupancy = true) {
   FusedMlpPlan p;
-  p.up = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN);
-  p.down = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED);
+  // the one launch runs the staged decode tiles; the two launches plan as lb_marlin_gemm does
+  p.up = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN, false, false);
+  p.down = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED, false, false);
+  const marlin::Plan up2 = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN);
+  const marlin::Plan down2 = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED);
   const bool wanted = mode == kMlpOne;
-  if (p.up.skinny && p.up.cpw >= 2 && p.down.skinny && p.down.splits <= mlp::kMaxSplits) {
+  // The one launch must sum every output as the two launches do (bit-identical
+  // results): only where both projections plan the same staged tiles.
+  auto same = [](const marlin::Plan& a, const marlin::Plan& b) {
+    return a.skinny && b.skinny && !b.direct && a.cpw == b.cpw && a.splits == b.splits;
+  };
+  if (p.up.skinny && p.up.cpw >= 2 && p.down.skinny && p.down.splits <= mlp::kMaxSplits && same(p.up, up2) &&
+      same(p.down, down2)) {
     p.wgs = std::max(p.up.n_cg * p.up.splits, p.down.n_cg * p.down.splits);
     p.lds = std::max(p.up.lds, p.down.lds);
     if (occupancy && wanted) {
@@ -657,10 +764,14 @@ FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g
   }
   // workspace: the hand-off counters and fault flag, then each projection's counters
   p.ws_up = mlp::kSyncWorkspace;
-  p.ws_down = p.ws_up + std::max<int64_t>(1 + std::max<int64_t>(p.up.n_cg, p.up.tail_tiles),
-                                           marlin::counters_needed(p.up, false));
-  p.ws_len = p.ws_down + std::max<int64_t>(1 + std::max<int64_t>(p.down.n_cg, p.down.tail_tiles),
-                                           marlin::counters_needed(p.down, false));
+  p.ws_down = p.ws_up + std::max(std::max<int64_t>(1 + std::max<int64_t>(p.up.n_cg, p.up.tail_tiles),
+                                                    marlin::counters_needed(p.up, false)),
+                                  std::max<int64_t>(1 + std::max<int64_t>(up2.n_cg, up2.tail_tiles),
+                                                    marlin::counters_needed(up2, false)));
+  p.ws_len = p.ws_down + std::max(std::max<int64_t>(1 + std::max<int64_t>(p.down.n_cg, p.down.tail_tiles),
+                                                    marlin::counters_needed(p.down, false)),
+                                  std::max<int64_t>(1 + std::max<int64_t>(down2.n_cg, down2.tail_tiles),
+                                                    marlin::counters_needed(down2, false)));
   return p;
 }
 

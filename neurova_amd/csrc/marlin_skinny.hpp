@@ -1,4 +1,4 @@
-// Marlin-layout W4A16 projection for skinny batches (decode: M <= 16) on gfx950.
+// Marlin-layout W4A16 projection for skinny batches (decode: M <= 32) on gfx950.
 //
 // Reads the reference's Marlin layout (langburst/csrc/marlin_cuda_kernel.cu,
 // packing in adapters/qwen36_tools/quantize.py:180-243) directly; no repack.
@@ -31,13 +31,17 @@
 // reference's fp16 (q - 8) * s, rounded as marlin_cuda_kernel.cu:131-159
 // rounds it; the MFMA then accumulates exact products in fp32.
 //
-// Latency.  The activation slice of the workgroup's k range is staged once in
-// LDS in fragment order ([k/32][4 k-groups][m] x 16 bytes, SiLU-gated
-// variant: fp16(silu(g) * u)); the staging loads are issued first and the
-// first weight batches (one scale group, 1 KB per wave each) right behind
-// them, so the staging round trip overlaps the weight fetch.  A ring of
-// kDepth batches stays in flight, with unconditional loads, so the memory
-// counters never force a full drain.
+// Latency.  M <= 16: the activation slice of the workgroup's k range is
+// staged once in LDS in fragment order ([k/32][4 k-groups][m] x 16 bytes,
+// SiLU-gated variant: fp16(silu(g) * u)); the staging loads are issued first
+// and the first weight batches (one scale group, 1 KB per wave each) right
+// behind them, so the staging round trip overlaps the weight fetch.  A ring
+// of kDepth batches stays in flight, with unconditional loads, so the memory
+// counters never force a full drain.  M = 17..32 (A_DIRECT, MR = 2 row blocks
+// of 16): staging the whole slice would hold every wave at the barrier for
+// twice the weight bytes, so each lane loads its own A fragments (16 bytes
+// per row block and step, from L2, completed by a lane swap) with the weight
+// batch they meet, in the same ring; no LDS, no barrier before the loop.
 
 // Epilogue.  Accumulators go through LDS so that thread t owns output column
 // t of the workgroup's 256.  Under split-K each workgroup publishes fp32
@@ -54,14 +58,16 @@ namespace skinny {
 constexpr int kWaves = 4;               // chunks (64 columns each) per workgroup
 constexpr int kThreads = kWaves * kWave;
 constexpr int kCols = 64 * kWaves;      // 256 columns per workgroup
-constexpr int kMaxM = 16;               // rows of the MFMA tile
+constexpr int kMaxM = 16;               // rows of the MFMA tile; the staged-A modes' M limit
+constexpr int kMaxMR = 2;               // A_DIRECT: 16-row blocks per MFMA tile (M <= 32)
 constexpr int kSteps = 4;               // 32-k steps per batch (one scale group)
 constexpr int kStageUnroll = 8;         // A staging: 16-byte items in flight per thread
 constexpr int kDepth = 2;               // weight batches in flight
 
 // A_HANDOFF: plain fp16 A written earlier in the same launch by other
 // workgroups (the fused MLP's activations), read with device-coherent loads.
-enum AMode { A_PLAIN = 0, A_SILU_PACKED = 1, A_HANDOFF = 2 };
+// A_DIRECT: plain fp16 A, not staged: fragments loaded per step (M up to 32).
+enum AMode { A_PLAIN = 0, A_SILU_PACKED = 1, A_HANDOFF = 2, A_DIRECT = 3 };
 // EPI_ACT: the tile pairs gate and up chunks (gate_up projection of an MLP)
 // and stores fp16(silu(g) * u) of its fp16 outputs instead of the outputs.
 enum EpiMode { EPI_STORE = 0, EPI_ARGMAX = 1, EPI_ACT = 2 };
@@ -140,19 +146,78 @@ __device__ __forceinline__ int tile_chunk(const Params& p, int cg, int c) {
   return cg * CPW + c;
 }
 
+// The split-K collect of a plain-store tile: sums the T shares of columns
+// [col0, col0 + 4 CQ) of every row in share order (deterministic), rounds to
+// fp16 (the per-column scale after that, as the reference does) and stores.
+// Thread t (of NT) takes column quad t % CQ and rows t / CQ + (NT / CQ) i, and
+// keeps every row's loads of up to kSU shares in flight together (16-byte
+// device-coherent loads, at most kMaxLoads per thread): the collect costs one
+// memory round trip per kSU shares, not one per four rows.
+template <bool GROUPED, int CQ, int NT, int ROWS, int kMaxLoads>
+__device__ __forceinline__ void collect_store(const Params& p, int total, int col0, int t) {
+  constexpr int kRowStep = NT / CQ;
+  constexpr int kRowIters = (ROWS + kRowStep - 1) / kRowStep;
+  constexpr int kSU = kMaxLoads / kRowIters < 1 ? 1 : kMaxLoads / kRowIters > 8 ? 8 : kMaxLoads / kRowIters;
+  const int mrows = p.m;
+  const int64_t share_stride = (int64_t)mrows * p.n;
+  // The partials of a skinny plan stay far below 4 GB (the planner keeps
+  // S * M * N small), so 32-bit buffer offsets address them.
+  const __amdgpu_buffer_rsrc_t rp = buffer_of(p.partial, (uint32_t)((int64_t)total * share_stride * 4));
+  const int cq = t % CQ, rs = t / CQ;
+  const int ncol = col0 + 4 * cq;
+  f32x4 sum[kRowIters];
+#pragma unroll
+  for (int i = 0; i < kRowIters; ++i) sum[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int s0 = 0; s0 < total; s0 += kSU) {
+    f32x4 tv[kRowIters][kSU];
+#pragma unroll
+    for (int i = 0; i < kRowIters; ++i)
+#pragma unroll
+      for (int u = 0; u < kSU; ++u) {
+        const int row = rs + kRowStep * i;
+        if (row < mrows) {
+          const int64_t e = (int64_t)min(s0 + u, total - 1) * share_stride + (int64_t)row * p.n + ncol;
+          tv[i][u] = collect16(rp, (uint32_t)(e * 4));
+        }
+      }
+#pragma unroll
+    for (int i = 0; i < kRowIters; ++i)
+#pragma unroll
+      for (int u = 0; u < kSU; ++u)
+        if (rs + kRowStep * i < mrows && s0 + u < total) sum[i] += tv[i][u];
+  }
+  f16 cs[4];
+#pragma unroll
+  for (int e = 0; e < 4; ++e)
+    cs[e] = GROUPED ? (f16)1.0f : __builtin_bit_cast(f16, p.s[per_column_scale_index(ncol + e)]);
+#pragma unroll
+  for (int i = 0; i < kRowIters; ++i) {
+    const int row = rs + kRowStep * i;
+    if (row < mrows) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        f16 h = (f16)sum[i][e];
+        if (!GROUPED) h = h * cs[e];
+        p.c[(int64_t)row * p.n + ncol + e] = __builtin_bit_cast(uint16_t, h);
+      }
+    }
+  }
+}
+
 // Plain-store epilogue, one wave on its own (no LDS, no workgroup barrier).
 // The wave holds the fp32 sums of one 64-column chunk over its share of K:
-// acc[j][i] is row 4 (lane >> 4) + i, column 16 j + (lane & 15) of the chunk.
-// Shares are the k splits times the k shares of a workgroup, T = S * ksub,
-// numbered split-major.  T == 1: the wave rounds and stores its outputs.
-// Otherwise it publishes its partial (device-coherent stores into
+// acc[rb][j][i] is row 16 rb + 4 (lane >> 4) + i, column 16 j + (lane & 15)
+// of the chunk.  Shares are the k splits times the k shares of a workgroup,
+// T = S * ksub, numbered split-major.  T == 1: the wave rounds and stores its
+// outputs.  Otherwise it publishes its partial (device-coherent stores into
 // partial [T][M][N]), waits for their acknowledgement, and counts its arrival
 // on the chunk's counter (workspace entry 1 + chunk); the wave that completes
 // the count reads the T partials of the chunk in share order (deterministic),
 // rounds, stores, and resets the counter.  Returns true in the wave that
 // stored the chunk's outputs.
-template <bool GROUPED>
-__device__ __forceinline__ bool wave_epilogue(const Params& p, const f32x4 (&acc)[4], int chunk, int share, int ksub) {
+template <bool GROUPED, int MR>
+__device__ __forceinline__ bool wave_epilogue(const Params& p, const f32x4 (&acc)[MR][4], int chunk, int share,
+                                              int ksub) {
   const int lane = threadIdx.x & 63;
   const int mrows = p.m;
   const int total = p.splits * ksub;
@@ -164,22 +229,26 @@ __device__ __forceinline__ bool wave_epilogue(const Params& p, const f32x4 (&acc
       const int n = col0 + 16 * j + (lane & 15);
       const f16 cs = GROUPED ? (f16)1.0f : __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = crow0 + i;
-        f16 h = (f16)acc[j][i];
-        if (!GROUPED) h = h * cs;
-        if (r < mrows) p.c[(int64_t)r * p.n + n] = __builtin_bit_cast(uint16_t, h);
-      }
+      for (int rb = 0; rb < MR; ++rb)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * rb + crow0 + i;
+          f16 h = (f16)acc[rb][j][i];
+          if (!GROUPED) h = h * cs;
+          if (r < mrows) p.c[(int64_t)r * p.n + n] = __builtin_bit_cast(uint16_t, h);
+        }
     }
     return true;
   }
   const int64_t share_stride = (int64_t)mrows * p.n;
   float* part = p.partial + share * share_stride + col0 + (lane & 15);
 #pragma unroll
-  for (int j = 0; j < 4; ++j)
+  for (int rb = 0; rb < MR; ++rb)
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      if (crow0 + i < mrows) publish(part + (int64_t)(crow0 + i) * p.n + 16 * j, acc[j][i]);
+    for (int j = 0; j < 4; ++j)
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (16 * rb + crow0 + i < mrows) publish(part + (int64_t)(16 * rb + crow0 + i) * p.n + 16 * j, acc[rb][j][i]);
   wait_published();
   int32_t* ctr = p.counters + 1 + chunk;
   int prev = 0;
@@ -187,31 +256,36 @@ __device__ __forceinline__ bool wave_epilogue(const Params& p, const f32x4 (&acc
   prev = __builtin_amdgcn_readfirstlane(prev);
   if (prev != total - 1) return false;
   if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  // lane = column of the chunk; 4 rows x 8 shares of loads in flight
-  const int n = col0 + lane;
-  const float* src = p.partial + n;
-  const f16 cs = GROUPED ? (f16)1.0f : __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
-  for (int r0 = 0; r0 < mrows; r0 += 4) {
+  if (MR == 1 && mrows <= 4) {
+    // Few rows: lane = column, the 4 rows x 8 shares of 4-byte loads in flight
+    // (one round trip up to 8 shares; measured faster here than the 16-byte
+    // form, which leaves 48 of the 64 lanes idle).
+    const int n = col0 + lane;
+    const float* src = p.partial + n;
+    const f16 cs = GROUPED ? (f16)1.0f : __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
     float sum[4] = {0.f, 0.f, 0.f, 0.f};
     for (int s0 = 0; s0 < total; s0 += 8) {
-      float t[4][8];
+      float tv[4][8];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int u = 0; u < 8; ++u)
-          t[i][u] = collect(src + (int64_t)min(s0 + u, total - 1) * share_stride + (int64_t)min(r0 + i, mrows - 1) * p.n);
+          tv[i][u] = collect(src + (int64_t)min(s0 + u, total - 1) * share_stride + (int64_t)min(i, mrows - 1) * p.n);
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int u = 0; u < 8; ++u) sum[i] += (s0 + u < total) ? t[i][u] : 0.f;
+        for (int u = 0; u < 8; ++u) sum[i] += (s0 + u < total) ? tv[i][u] : 0.f;
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       f16 h = (f16)sum[i];
       if (!GROUPED) h = h * cs;
-      if (r0 + i < mrows) p.c[(int64_t)(r0 + i) * p.n + n] = __builtin_bit_cast(uint16_t, h);
+      if (i < mrows) p.c[(int64_t)i * p.n + n] = __builtin_bit_cast(uint16_t, h);
     }
+    return true;
   }
+  // (MR = 2: fewer loads in flight, so that two workgroups still fit a CU)
+  collect_store<GROUPED, 16, kWave, 16 * MR, MR == 1 ? 32 : 16>(p, total, col0, lane);
   return true;
 }
 
@@ -227,9 +301,13 @@ struct NoWait {
 // until A has been written, then A is staged.  Returns true in the workgroup
 // that stored the tile's outputs (EPI_STORE, EPI_ACT) or ran the launch's
 // final argmax reduction.
-template <int AM, int EPI, bool GROUPED, int CPW, typename WaitA = NoWait>
+template <int AM, int EPI, bool GROUPED, int CPW, int MR = 1, typename WaitA = NoWait>
 __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const int split, WaitA wait_for_a = WaitA()) {
   static_assert(EPI != EPI_ACT || CPW >= 2, "EPI_ACT pairs a gate and an up chunk");
+  static_assert(MR == 1 || (AM == A_DIRECT && EPI == EPI_STORE), "row blocks > 1: direct A, plain store");
+  static_assert(MR >= 1 && MR <= kMaxMR, "row blocks");
+  constexpr bool kDirect = AM == A_DIRECT;
+  constexpr int kRows = 16 * MR;  // rows of the MFMA tile
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int s_prev;
   __shared__ uint64_t s_keys[kWaves][kMaxM];
@@ -242,7 +320,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int mrows = p.m;      // <= kMaxM
+  const int mrows = p.m;      // <= kRows
   constexpr int cpw = CPW;
   constexpr int ksub = kWaves / cpw;   // k shares per tile
   const int wchunk = cpw == kWaves ? wave : (wave & (cpw - 1));  // this wave's chunk of the tile ...
@@ -319,52 +397,73 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     }
   };
 
+  // A_DIRECT: lane (g, row mrow) of row block rb needs row min(16 rb + mrow,
+  // M - 1) (rows >= M compute values that are never stored) at k offsets
+  // 32 kp + 16 prow + 4 gq + {0..3} and the same + 8 (the staged entry's
+  // contents).  It loads the 16 contiguous bytes at 32 kp + 16 prow + 8 gq
+  // instead; the lanes of gq = 0 and gq = 1 (rows 2 prow and 2 prow + 1 of the
+  // wave) then hold each other's missing halves, which two
+  // v_permlane16_swap exchange at use.
+  const uint16_t* arow[MR];
+#pragma unroll
+  for (int rb = 0; rb < MR; ++rb)
+    arow[rb] = p.a + (int64_t)min(16 * rb + mrow, mrows - 1) * p.k + 16 * prow + 8 * gq;
+
   // Ring of kDepth batches (one scale group, 1 KB per wave, each) in flight.
   u32x4 bw[kDepth][kSteps];
   u32x4 bs[kDepth];
+  u32x4 aw[kDepth][kSteps][MR];  // A_DIRECT only
 #pragma unroll
   for (int i = 0; i < kDepth; ++i) bs[i] = (u32x4){0, 0, 0, 0};
-  auto issue = [&](u32x4(&w)[kSteps], u32x4& scl, int batch) {
+  auto issue = [&](int slot, int batch) __attribute__((always_inline)) {
     const int kpf = kpw0 + batch * kSteps;
 #pragma unroll
     for (int d = 0; d < kSteps; ++d) {
       const u32x4* src = reinterpret_cast<const u32x4*>(bsrc + (int64_t)(kpf + d) * 2 * row_words);
-      w[d] = *src;
+      bw[slot][d] = *src;
+      if constexpr (kDirect) {
+#pragma unroll
+        for (int rb = 0; rb < MR; ++rb) aw[slot][d][rb] = *reinterpret_cast<const u32x4*>(arow[rb] + 32 * (kpf + d));
+      }
     }
-    if (GROUPED) scl = *reinterpret_cast<const u32x4*>(ssrc + (int64_t)(kpf >> 2) * p.n);
+    if (GROUPED) bs[slot] = *reinterpret_cast<const u32x4*>(ssrc + (int64_t)(kpf >> 2) * p.n);
   };
 
   // ---- staging loads, then the first weight batches, then the stores ----
-  // (A_HANDOFF: the weight batches first, then the wait for A)
-  if (AM != A_HANDOFF) stage_load(0);
+  // (A_HANDOFF: the weight batches first, then the wait for A; A_DIRECT: no staging)
+  if (AM != A_HANDOFF && !kDirect) stage_load(0);
   __builtin_amdgcn_sched_barrier(0);  // staging loads strictly before the weight loads
 #pragma unroll
   for (int i = 0; i < kDepth; ++i) {
-    issue(bw[i], bs[i], min(i, nb - 1));
+    issue(i, min(i, nb - 1));
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: the loop's waits assume it
   }
   if (AM == A_HANDOFF) {
     wait_for_a();
     stage_load(0);
   }
-  __builtin_amdgcn_sched_barrier(0);
-  stage_store(0);
-  for (int base = kThreads * kStageUnroll; base < items; base += kThreads * kStageUnroll) {
-    stage_load(base);
-    stage_store(base);
+  if constexpr (!kDirect) {
+    __builtin_amdgcn_sched_barrier(0);
+    stage_store(0);
+    for (int base = kThreads * kStageUnroll; base < items; base += kThreads * kStageUnroll) {
+      stage_load(base);
+      stage_store(base);
+    }
+    if (tid == 0) afr[n_frag] = (u32x4){0, 0, 0, 0};
+    lds_barrier();  // LDS only: the weight ring stays in flight
   }
-  if (tid == 0) afr[n_frag] = (u32x4){0, 0, 0, 0};
-  lds_barrier();  // LDS only: the weight ring stays in flight
 
   // A fragment address: rows >= M read the zero entry.
   const bool a_live = mrow < mrows;
   const int a_step = a_live ? 4 * mrows : 0;
   const int a_base = a_live ? g * mrows + mrow + gw0 * kSteps * a_step : n_frag;
-  const int crow0 = (lane >> 4) * 4;  // accumulator rows of this lane
+  const int crow0 = (lane >> 4) * 4;  // accumulator rows of this lane (within a row block)
 
-  f32x4 acc[4];
+  f32x4 acc[MR][4];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) acc[j] = (f32x4){0.f, 0.f, 0.f, 0.f};
+  for (int rb = 0; rb < MR; ++rb)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) acc[rb][j] = (f32x4){0.f, 0.f, 0.f, 0.f};
 
   // One batch = one scale group.  The weights are the reference's fp16
   // fp16(q - 8) * s (marlin_cuda_kernel.cu:131-159: exact q - 8 from one
@@ -372,7 +471,8 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   // group's scale), so every product with an fp16 activation is exact in the
   // fp32 MFMA accumulation, as in the reference's MMA.  Per-column scales: the
   // exact q - 8, scaled after the fp16 rounding of the sum.
-  auto consume = [&](const u32x4(&w)[kSteps], const u32x4& scl, int batch) {
+  auto consume = [&](int slot, int batch) __attribute__((always_inline)) {
+    const u32x4 scl = bs[slot];
     f16x2 sc2[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {  // column 16j + 8h + c
@@ -381,9 +481,21 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     }
 #pragma unroll
     for (int d = 0; d < kSteps; ++d) {
-      const u32x4 t = afr[a_base + (batch * kSteps + d) * a_step];
-      const f16x8 afrag = __builtin_bit_cast(f16x8, t);
-      const u32x4 own = w[d];
+      f16x8 afrag[MR];
+      if constexpr (kDirect) {
+#pragma unroll
+        for (int rb = 0; rb < MR; ++rb) {
+          // odd rows of word 0 (gq = 1: halves 8, 9) <-> even rows of word 2
+          // (gq = 0: halves 4, 5); the same for words 1 and 3
+          const u32x4 l = aw[slot][d][rb];
+          const auto w02 = __builtin_amdgcn_permlane16_swap(l[0], l[2], false, false);
+          const auto w13 = __builtin_amdgcn_permlane16_swap(l[1], l[3], false, false);
+          afrag[rb] = __builtin_bit_cast(f16x8, (u32x4){w02[0], w13[0], w02[1], w13[1]});
+        }
+      } else {
+        afrag[0] = __builtin_bit_cast(f16x8, afr[a_base + (batch * kSteps + d) * a_step]);
+      }
+      const u32x4 own = bw[slot][d];
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
         const uint32_t partner = (uint32_t)__builtin_amdgcn_mov_dpp((int)own[j], 0x128, 0xf, 0xf, false);  // row_ror:8
@@ -398,7 +510,9 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
           h1 *= sc2[j];
         }
         const f16x8 bfrag = __builtin_bit_cast(f16x8, make_uint4(as_u32(l0), as_u32(l1), as_u32(h0), as_u32(h1)));
-        acc[j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag, bfrag, acc[j], 0, 0, 0);
+#pragma unroll
+        for (int rb = 0; rb < MR; ++rb)
+          acc[rb][j] = __builtin_amdgcn_mfma_f32_16x16x32_f16(afrag[rb], bfrag, acc[rb][j], 0, 0, 0);
       }
     }
   };
@@ -412,37 +526,39 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   for (; b + 2 * kDepth <= nb; b += kDepth) {
 #pragma unroll
     for (int i = 0; i < kDepth; ++i) {
-      consume(bw[i], bs[i], b + i);
+      consume(i, b + i);
       __builtin_amdgcn_sched_barrier(0);
-      issue(bw[i], bs[i], b + i + kDepth);
+      issue(i, b + i + kDepth);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 #pragma unroll
   for (int i = 0; i < kDepth; ++i) {
     if (b + i < nb) {
-      consume(bw[i], bs[i], b + i);
-      if (b + i + kDepth < nb) issue(bw[i], bs[i], b + i + kDepth);
+      consume(i, b + i);
+      if (b + i + kDepth < nb) issue(i, b + i + kDepth);
     }
   }
 #pragma unroll
   for (int i = 0; i < kDepth - 1; ++i)
-    if (b + kDepth + i < nb) consume(bw[i], bs[i], b + kDepth + i);
+    if (b + kDepth + i < nb) consume(i, b + kDepth + i);
 
   // Wide tiles (each wave its own chunk): the wave hands off on its own.
-  if constexpr (EPI == EPI_STORE && CPW == kWaves) return wave_epilogue<GROUPED>(p, acc, chunk, split, 1);
+  if constexpr (EPI == EPI_STORE && CPW == kWaves) return wave_epilogue<GROUPED, MR>(p, acc, chunk, split, 1);
 
   // ---- epilogue: accumulators -> LDS tile [mrows][256] fp32 ----
-  __syncthreads();  // every wave is done with the staged A
+  if constexpr (!kDirect) __syncthreads();  // every wave is done with the staged A
   float* tile = reinterpret_cast<float*>(smem);
   {
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int rb = 0; rb < MR; ++rb)
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = crow0 + i;
-        if (r < mrows) tile[r * kCols + wave * 64 + 16 * j + (lane & 15)] = acc[j][i];
-      }
+      for (int j = 0; j < 4; ++j)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const int r = 16 * rb + crow0 + i;
+          if (r < mrows) tile[r * kCols + wave * 64 + 16 * j + (lane & 15)] = acc[rb][j][i];
+        }
   }
   __syncthreads();
   // Thread t < 64 * cpw owns column t of the tile: the sum of its k shares
@@ -451,9 +567,9 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   // this thread's output column
   const int n = EPI == EPI_ACT ? (col_live ? tile_chunk<EPI, CPW>(p, cg, tid >> 6) * 64 + (tid & 63) : 0)
                                : cg * 64 * cpw + (col_live ? tid : 0);
-  float v[kMaxM];
+  float v[kRows];
 #pragma unroll
-  for (int r = 0; r < kMaxM; ++r) {
+  for (int r = 0; r < kRows; ++r) {
     float t = 0.f;
     if (r < mrows && col_live) {
       t = tile[r * kCols + tid];  // share 0 (wave tid / 64)
@@ -465,7 +581,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   if (p.splits > 1) {
     float* part = p.partial + (int64_t)split * p.m * p.n + n;
 #pragma unroll
-    for (int r = 0; r < kMaxM; ++r)
+    for (int r = 0; r < kRows; ++r)
       if (r < mrows && col_live) publish(part + (int64_t)r * p.n, v[r]);
     wait_published();
     __syncthreads();
@@ -474,11 +590,15 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     __syncthreads();
     if (s_prev != p.splits - 1) return false;  // not the last split of this tile
     if (tid == 0) reset_counter(ctr);
+    if constexpr (EPI == EPI_STORE) {  // every thread of the workgroup collects
+      collect_store<GROUPED, 16 * CPW, kThreads, kRows, 32>(p, p.splits, cg * 64 * cpw, tid);
+      return true;
+    }
     // Sum the partials in split order; 4 rows x 8 splits of reads in flight.
     const float* src = p.partial + n;
     const int64_t split_stride = (int64_t)p.m * p.n;
 #pragma unroll
-    for (int r0 = 0; r0 < kMaxM; r0 += 4) {
+    for (int r0 = 0; r0 < kRows; r0 += 4) {
       if (r0 < mrows && col_live) {
         float sum[4] = {0.f, 0.f, 0.f, 0.f};
         for (int s0 = 0; s0 < p.splits; s0 += 8) {
@@ -503,9 +623,9 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   // fp16 rounding (per-column scale after it, as the reference does)
   f16 colscale = (f16)1.0f;
   if (!GROUPED && col_live) colscale = __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
-  uint16_t outh[kMaxM];
+  uint16_t outh[kRows];
 #pragma unroll
-  for (int r = 0; r < kMaxM; ++r) {
+  for (int r = 0; r < kRows; ++r) {
     f16 h = (f16)v[r];
     if (!GROUPED) h = h * colscale;
     outh[r] = __builtin_bit_cast(uint16_t, h);
@@ -513,7 +633,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
 
   if (EPI == EPI_STORE) {
 #pragma unroll
-    for (int r = 0; r < kMaxM; ++r)
+    for (int r = 0; r < kRows; ++r)
       if (r < mrows && col_live) p.c[(int64_t)r * p.n + n] = outh[r];
     return true;
   }
@@ -526,7 +646,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     uint16_t* xch = reinterpret_cast<uint16_t*>(smem);
     __syncthreads();  // every thread is done with the fp32 tile
 #pragma unroll
-    for (int r = 0; r < kMaxM; ++r)
+    for (int r = 0; r < kRows; ++r)
       if (r < mrows && col_live) xch[r * kTileCols + tid] = outh[r];
     __syncthreads();
     const uint32_t* xw = reinterpret_cast<const uint32_t*>(xch);
@@ -577,7 +697,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
 // preloads the leading kernel arguments into SGPRs at wave launch (the build
 // asks for 16 dwords), so the first weight loads do not wait for a kernarg
 // fetch.  A struct argument is not preloaded.
-template <int AM, int EPI, bool GROUPED, int CPW>
+template <int AM, int EPI, bool GROUPED, int CPW, int MR = 1>
 __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(const uint16_t* a, const uint32_t* b,
                                                                  const uint16_t* s, uint16_t* c, int32_t* counters,
                                                                  float* partial, int m, int n, int k, int splits,
@@ -587,7 +707,23 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(const uint16_t*
   p.a = a; p.b = b; p.s = s; p.c = c; p.counters = counters; p.partial = partial;
   p.m = m; p.n = n; p.k = k; p.splits = splits; p.kp_total = k >> 5; p.n_cg = n_cg;
   p.tile_keys = tile_keys; p.argmax_state = argmax_state; p.argmax_out = argmax_out;
-  skinny_tile<AM, EPI, GROUPED, CPW>(p, blockIdx.x, blockIdx.y);
+  skinny_tile<AM, EPI, GROUPED, CPW, MR>(p, blockIdx.x, blockIdx.y);
+}
+
+// SiLU-gated activations for the A_DIRECT launches: act[m][k] =
+// fp16(silu(g) * u) of mixed [M, 2K] = [g | u], with the staging's own
+// function (silu_mul2), so the direct launch sees the values the staged
+// A_SILU_PACKED variant would.  One thread per 8 halves.
+__global__ __launch_bounds__(256) void silu_pack_kernel(const uint16_t* __restrict__ mixed, uint16_t* __restrict__ act,
+                                                        int m, int k) {
+  const int64_t octs = (int64_t)k >> 3;
+  const int64_t it = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (it >= (int64_t)m * octs) return;
+  const int64_t row = it / octs, o = it - row * octs;
+  const uint4 g = *reinterpret_cast<const uint4*>(mixed + row * 2 * k + 8 * o);
+  const uint4 u = *reinterpret_cast<const uint4*>(mixed + row * 2 * k + k + 8 * o);
+  *reinterpret_cast<uint4*>(act + row * k + 8 * o) =
+      make_uint4(silu_mul2(g.x, u.x), silu_mul2(g.y, u.y), silu_mul2(g.z, u.z), silu_mul2(g.w, u.w));
 }
 
 }  // namespace skinny

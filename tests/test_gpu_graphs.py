@@ -37,9 +37,10 @@ def _replay_and_check(torch, graph, outs, eager, ws_list, disturb):
             assert int(ws.abs().sum()) == 0, f"replay {rep} left the workspace non-zero"
 
 
-@pytest.mark.parametrize("m,k,n", [(1, 5120, 17408), (4, 17408, 5120), (64, 5120, 4096)])
+@pytest.mark.parametrize("m,k,n", [(1, 5120, 17408), (4, 17408, 5120), (32, 5120, 7168), (64, 5120, 4096)])
 def test_marlin_gemm_graph_replay(dev, m, k, n):
-    """Decode (split-K, counters in the workspace) and prefill (tail splits) launches."""
+    """Decode (split-K, counters in the workspace; M = 32: A fragments loaded per
+    step) and prefill (tail splits) launches."""
     import torch
     import langburst_cuda as lc
 
@@ -67,11 +68,14 @@ def test_marlin_gemm_graph_replay(dev, m, k, n):
                       lambda: lc.lowbit_marlin_gemm_out(q, s, x, other, ws, k, 128))
 
 
-def test_silu_packed_graph_replay(dev):
+@pytest.mark.parametrize("m", [2, 32])
+def test_silu_packed_graph_replay(dev, m):
+    """M = 32 captures two launches: the SiLU-gated activations formed once
+    into scratch, then the direct-A decode kernel over them."""
     import torch
     import langburst_cuda as lc
 
-    m, k, n = 2, 17408, 5120
+    k, n = 17408, 5120
     print_case("graph-silu", m, k, n)
     gen = torch.Generator(device=dev)
     gen.manual_seed(9)

@@ -82,7 +82,7 @@ def _assert_per_column_rounding(got, codes, x, sp):
 
 
 @pytest.mark.parametrize("group", [128, -1])
-@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 16])
+@pytest.mark.parametrize("m", [1, 2, 3, 4, 7, 16, 17, 24, 32])
 @pytest.mark.parametrize("k,n", [(256, 256), (1024, 512), (512, 1280)])
 def test_skinny_vs_oracle(dev, m, k, n, group):
     print_case("skinny", m, k, n, group)
@@ -169,7 +169,7 @@ def test_gemm_vs_oracle(dev, m):
     got = _run_gemm(dev, x, qw, sp, 128)
     ref = O.marlin_gemm(x, qw, sp, 128)
     exact = assert_close_f16(got, ref, what=f"m={m}")
-    if m <= 16:  # decode kernel
+    if m <= 32:  # decode kernel (M = 17..32: A fragments loaded per step)
         assert_reference_rounding(got, ref, x, qw, sp, 128, what=f"m={m}")
     else:  # prefill kernel: the reference's fp16 (q - 8) * s weights
         assert exact > 0.95
@@ -248,8 +248,9 @@ def test_narrow_silu_and_argmax_vs_oracle(dev, m, k, n):
 
 @pytest.mark.parametrize("m", [32, 48])
 def test_small_m_gemm_many_splits_vs_oracle(dev, m):
-    """M just above the decode kernel's 16 rows on the down projection (K = 17408,
-    N = 5120): few tiles, so the prefill kernel splits K many ways (13 at M = 32);
+    """M above 16 rows on the down projection (K = 17408, N = 5120): at M = 32 the
+    decode kernel with A fragments loaded per step (the SiLU-gated activations
+    formed once first), at M = 48 the prefill kernel split many ways over K;
     plain and SiLU-gated A, workspace left zero."""
     import torch
     from neurova_amd import capi

@@ -121,7 +121,9 @@ def test_fused_mlp_model_shape_one_launch(dev, batch):
 
     launches = capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128, capi.MLP_ONE_LAUNCH)
     print_case("mlp_fused_model", batch, "launches", launches)
-    assert launches == 1
+    # batch 16: the two launches take direct-A tiles the one-launch kernel does
+    # not have, so mode 1 runs them too (the output stays bit-identical)
+    assert launches == (1 if batch <= 4 else 2)
     # auto: always the two launches (the one launch is opt-in)
     assert capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128) == 2
     args = _problem_dev(HIDDEN, INTER, batch, 7 + batch, dev)
