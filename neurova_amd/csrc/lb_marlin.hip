@@ -158,7 +158,8 @@ inline size_t align_up(size_t v) { return (v + kAlign - 1) & ~(kAlign - 1); }
 
 struct Plan {
   bool skinny = true;
-  bool direct = false; // decode kernel with A fragments loaded per step (skinny::A_DIRECT)
+  bool direct = false; // decode kernel without the whole-slice A staging: A fragments loaded per
+                       // step (skinny::A_DIRECT), or, on 4-chunk tiles, an LDS ring (skinny::A_RING)
   int mr = 1;          // decode: 16-row blocks of the MFMA tile
   int mb = 1;        // GEMM: 16-row blocks per workgroup
   int n_mb = 1;
@@ -267,10 +268,11 @@ inline Tiling staged_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
   return t;
 }
 
-// Direct A: every workgroup reads its A fragments itself, so the split cap
-// S * M <= K / 32 bites early at larger M; the widest tiling that gives 1.5
-// workgroups per CU within kSkinnyMaxSplits splits, else the one with the
-// most workgroups.
+// Without the whole-slice staging: the split cap S * M <= K / 32 bites early
+// at larger M; the widest tiling within kSkinnyMaxSplits splits that gives
+// every CU a workgroup (4-chunk tiles, whose waves share A through the LDS
+// ring) or 1.5 workgroups per CU (narrower tiles, each wave loading its own
+// A), else the one with the most workgroups.
 inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
   Tiling t;
   int64_t most = -1;
@@ -278,7 +280,8 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
     const int sc = skinny_splits(m, n, k, workspace_len, c, true);
     if (sc == 0) continue;
     const int64_t w = (n / (64 * c)) * sc;
-    if (sc <= kSkinnyMaxSplits && 2 * w >= 3 * (int64_t)device_cus()) return Tiling{c, sc};
+    const int64_t fill = c == skinny::kWaves ? device_cus() : 3 * (int64_t)device_cus() / 2;
+    if (sc <= kSkinnyMaxSplits && w >= fill) return Tiling{c, sc};
     if (w > most) {
       most = w;
       t = Tiling{c, sc};
@@ -295,10 +298,11 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // form where the tiles are narrow (the waves of a workgroup then share
 // little A, and staging the whole slice before the loop holds them up), or
 // where LDS forces the staged form to more splits than one wave of resident
-// workgroups; the staged form where 4-chunk tiles share the slice.  The
-// SiLU-gated direct form first forms fp16(silu(g) * u) in a launch of its
-// own, which does not pay below 5 rows.  M = 17..32: the direct form on
-// 64-column tiles only; wider tiles go to the prefill kernel.
+// workgroups (on 4-chunk tiles, A then goes through the LDS ring); the
+// staged form where 4-chunk tiles share the slice.  The SiLU-gated direct
+// form first forms fp16(silu(g) * u) in a launch of its own, which does not
+// pay below 5 rows.  M = 17..32: the direct form on 64-column tiles, the
+// ring on 4-chunk tiles; 2-chunk tiles go to the prefill kernel.
 inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am, bool argmax = false,
                       bool allow_direct = true) {
   Plan pl;
@@ -309,7 +313,7 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
                                                                          : Tiling{};
   bool direct = false;
   if (td.cpw > 0) {
-    if (m > skinny::kMaxM) direct = td.cpw == 1;
+    if (m > skinny::kMaxM) direct = td.cpw != 2;
     else if (ts.cpw == 0) direct = true;
     else if (am == gemm::A_SILU_PACKED && m <= 4) direct = false;
     else direct = td.cpw <= 2 || (ts.cpw == td.cpw && ts.s > td.s);
@@ -328,7 +332,9 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
     const size_t stage = direct ? 0 : pl.x_bytes + 16;                   // + the zero entry
     // the epilogue's fp32 tile [M][256] (direct plans on wide tiles store per wave)
     const size_t tile = (direct && cpw == skinny::kWaves) ? 0 : (size_t)m * skinny::kCols * 4;
-    pl.lds = std::max(stage, tile);
+    // A_RING: two batches of [M][128 k] in fragment order + the zero entry
+    const size_t ring = (direct && cpw == skinny::kWaves) ? (size_t)(32 * m + 1) * 16 : 0;
+    pl.lds = std::max(std::max(stage, tile), ring);
     pl.partial_bytes = pl.splits > 1 ? align_up((size_t)pl.splits * (size_t)m * (size_t)n * 4) : 0;
     if (direct && am == gemm::A_SILU_PACKED) pl.act_bytes = align_up((size_t)m * (size_t)k * 2);
   } else {
@@ -431,24 +437,25 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
     }
     const int32_t sp = pl.splits, ncg = pl.n_cg;
     dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
-#define LB_SKD(GV, CV, MRV)                                                                                       \
-  hipLaunchKernelGGL((skinny::marlin_skinny_kernel<skinny::A_DIRECT, skinny::EPI_STORE, GV, CV, MRV>), grid,     \
+#define LB_SKD(AMV, GV, CV, MRV)                                                                                  \
+  hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, skinny::EPI_STORE, GV, CV, MRV>), grid,                  \
                      dim3(skinny::kThreads), pl.lds, st, av, reinterpret_cast<const uint32_t*>(b), s, c, workspace, \
                      partial, (int)m, (int)n, (int)k, sp, ncg, nullptr, nullptr, nullptr)
-#define LB_SKDC(GV, MRV)                          \
-  do {                                            \
-    if (pl.cpw == 4) LB_SKD(GV, 4, MRV);          \
-    else if (pl.cpw == 2) LB_SKD(GV, 2, MRV);     \
-    else LB_SKD(GV, 1, MRV);                      \
+#define LB_SKDG(AMV, CV, MRV)                               \
+  do {                                                      \
+    if (grouped) LB_SKD(AMV, true, CV, MRV);                \
+    else LB_SKD(AMV, false, CV, MRV);                       \
   } while (0)
-    if (pl.mr == 1) {
-      if (grouped) LB_SKDC(true, 1);
-      else LB_SKDC(false, 1);
-    } else {  // M = 17..32: 64-column tiles only (make_plan)
-      if (grouped) LB_SKD(true, 1, 2);
-      else LB_SKD(false, 1, 2);
+    if (pl.cpw == 4) {  // 4-chunk tiles: A through the LDS ring
+      if (pl.mr == 1) LB_SKDG(skinny::A_RING, 4, 1);
+      else LB_SKDG(skinny::A_RING, 4, 2);
+    } else if (pl.mr == 1) {
+      if (pl.cpw == 2) LB_SKDG(skinny::A_DIRECT, 2, 1);
+      else LB_SKDG(skinny::A_DIRECT, 1, 1);
+    } else {  // M = 17..32: 64-column tiles (make_plan)
+      LB_SKDG(skinny::A_DIRECT, 1, 2);
     }
-#undef LB_SKDC
+#undef LB_SKDG
 #undef LB_SKD
     return lbh::launch_status();
   }

@@ -67,7 +67,9 @@ constexpr int kDepth = 2;               // weight batches in flight
 // A_HANDOFF: plain fp16 A written earlier in the same launch by other
 // workgroups (the fused MLP's activations), read with device-coherent loads.
 // A_DIRECT: plain fp16 A, not staged: fragments loaded per step (M up to 32).
-enum AMode { A_PLAIN = 0, A_SILU_PACKED = 1, A_HANDOFF = 2, A_DIRECT = 3 };
+// A_RING: plain fp16 A staged one batch (one scale group) at a time through a
+// two-slot LDS ring, for 4-chunk tiles whose waves share it (M up to 32).
+enum AMode { A_PLAIN = 0, A_SILU_PACKED = 1, A_HANDOFF = 2, A_DIRECT = 3, A_RING = 4 };
 // EPI_ACT: the tile pairs gate and up chunks (gate_up projection of an MLP)
 // and stores fp16(silu(g) * u) of its fp16 outputs instead of the outputs.
 enum EpiMode { EPI_STORE = 0, EPI_ARGMAX = 1, EPI_ACT = 2 };
@@ -304,9 +306,11 @@ struct NoWait {
 template <int AM, int EPI, bool GROUPED, int CPW, int MR = 1, typename WaitA = NoWait>
 __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const int split, WaitA wait_for_a = WaitA()) {
   static_assert(EPI != EPI_ACT || CPW >= 2, "EPI_ACT pairs a gate and an up chunk");
-  static_assert(MR == 1 || (AM == A_DIRECT && EPI == EPI_STORE), "row blocks > 1: direct A, plain store");
+  static_assert(MR == 1 || ((AM == A_DIRECT || AM == A_RING) && EPI == EPI_STORE), "row blocks > 1: plain store");
   static_assert(MR >= 1 && MR <= kMaxMR, "row blocks");
+  static_assert(AM != A_RING || (CPW == kWaves && EPI == EPI_STORE), "A ring: 4-chunk plain-store tiles");
   constexpr bool kDirect = AM == A_DIRECT;
+  constexpr bool kRing = AM == A_RING;
   constexpr int kRows = 16 * MR;  // rows of the MFMA tile
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int s_prev;
@@ -409,6 +413,39 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   for (int rb = 0; rb < MR; ++rb)
     arow[rb] = p.a + (int64_t)min(16 * rb + mrow, mrows - 1) * p.k + 16 * prow + 8 * gq;
 
+  // A_RING: batch b of the workgroup's A (rows x 128 k, fragment order as
+  // staged above) lives in LDS slot b & 1; thread t loads 16-byte items
+  // t + 256 u (row it >> 4, octet it & 15) of batch b + 1 two batches ahead
+  // into registers, stores them while batch b is consumed, and one LDS barrier
+  // per batch publishes them (and frees the slot of batch b - 1).
+  constexpr int kRingItems = (16 * kRows + kThreads - 1) / kThreads;
+  const int ring_slot = 16 * mrows;  // fragment entries per slot
+  const int ring_zero = 2 * ring_slot;
+  u32x4 ar[kDepth][kRingItems];
+  u32x4 ar0[kRingItems];
+  auto ring_load = [&](u32x4(&dst)[kRingItems], int batch) __attribute__((always_inline)) {
+    const int kb = 32 * (kpw0 + batch * kSteps);
+#pragma unroll
+    for (int u = 0; u < kRingItems; ++u) {
+      const int it = tid + kThreads * u;
+      const int mm = min(it >> 4, mrows - 1);
+      dst[u] = *reinterpret_cast<const u32x4*>(p.a + (int64_t)mm * p.k + kb + 8 * (it & 15));
+    }
+  };
+  auto ring_store = [&](const u32x4(&src)[kRingItems], int lslot) __attribute__((always_inline)) {
+#pragma unroll
+    for (int u = 0; u < kRingItems; ++u) {
+      const int it = tid + kThreads * u;
+      const int mm = it >> 4, o = it & 15;  // o = 4 d + 2 prow + half
+      if (mm < mrows) {
+        const int fg = lslot * ring_slot + ((o >> 2) * 4 + ((o & 3) >> 1) * 2) * mrows + mm;
+        uint2* dst = reinterpret_cast<uint2*>(afr + fg) + (o & 1);
+        dst[0] = make_uint2(src[u][0], src[u][1]);          // halves 0..3 -> g = 2 prow
+        dst[2 * mrows] = make_uint2(src[u][2], src[u][3]);  // halves 4..7 -> g = 2 prow + 1
+      }
+    }
+  };
+
   // Ring of kDepth batches (one scale group, 1 KB per wave, each) in flight.
   u32x4 bw[kDepth][kSteps];
   u32x4 bs[kDepth];
@@ -430,19 +467,28 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   };
 
   // ---- staging loads, then the first weight batches, then the stores ----
-  // (A_HANDOFF: the weight batches first, then the wait for A; A_DIRECT: no staging)
-  if (AM != A_HANDOFF && !kDirect) stage_load(0);
+  // (A_HANDOFF: the weight batches first, then the wait for A; A_DIRECT: no
+  // staging; A_RING: batch 0 of A, then per weight batch i the A batch i + 1)
+  if (AM != A_HANDOFF && !kDirect && !kRing) stage_load(0);
+  if constexpr (kRing) ring_load(ar0, 0);
   __builtin_amdgcn_sched_barrier(0);  // staging loads strictly before the weight loads
 #pragma unroll
   for (int i = 0; i < kDepth; ++i) {
     issue(i, min(i, nb - 1));
+    if constexpr (kRing) ring_load(ar[i], min(i + 1, nb - 1));
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: the loop's waits assume it
   }
   if (AM == A_HANDOFF) {
     wait_for_a();
     stage_load(0);
   }
-  if constexpr (!kDirect) {
+  if constexpr (kRing) {
+    __builtin_amdgcn_sched_barrier(0);
+    ring_store(ar0, 0);
+    if (tid == 0) afr[ring_zero] = (u32x4){0, 0, 0, 0};
+    lds_barrier();  // LDS only: the weight ring stays in flight
+  }
+  if constexpr (!kDirect && !kRing) {
     __builtin_amdgcn_sched_barrier(0);
     stage_store(0);
     for (int base = kThreads * kStageUnroll; base < items; base += kThreads * kStageUnroll) {
@@ -458,6 +504,15 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   const int a_step = a_live ? 4 * mrows : 0;
   const int a_base = a_live ? g * mrows + mrow + gw0 * kSteps * a_step : n_frag;
   const int crow0 = (lane >> 4) * 4;  // accumulator rows of this lane (within a row block)
+  // A_RING fragment addresses per row block (rows >= M read the zero entry)
+  int r_base[MR], r_step[MR], r_slot[MR];
+#pragma unroll
+  for (int rb = 0; rb < MR; ++rb) {
+    const bool live = 16 * rb + mrow < mrows;
+    r_base[rb] = live ? g * mrows + 16 * rb + mrow : ring_zero;
+    r_step[rb] = live ? 4 * mrows : 0;
+    r_slot[rb] = live ? ring_slot : 0;
+  }
 
   f32x4 acc[MR][4];
 #pragma unroll
@@ -492,6 +547,10 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
           const auto w13 = __builtin_amdgcn_permlane16_swap(l[1], l[3], false, false);
           afrag[rb] = __builtin_bit_cast(f16x8, (u32x4){w02[0], w13[0], w02[1], w13[1]});
         }
+      } else if constexpr (kRing) {
+#pragma unroll
+        for (int rb = 0; rb < MR; ++rb)
+          afrag[rb] = __builtin_bit_cast(f16x8, afr[r_base[rb] + (batch & 1) * r_slot[rb] + d * r_step[rb]]);
       } else {
         afrag[0] = __builtin_bit_cast(f16x8, afr[a_base + (batch * kSteps + d) * a_step]);
       }
@@ -522,6 +581,17 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   // The scheduling barriers keep each re-issue right after the consume that
   // frees its slot (the scheduler would otherwise sink all loads to the end of
   // the round and expose a full memory latency per round).
+  // A_RING, after consuming batch bb from slot i: A register slot i holds
+  // batch bb + 1; store it to LDS slot (bb + 1) & 1 (whose batch bb - 1 every
+  // wave finished before the last barrier), reload the register slot with
+  // batch bb + 1 + kDepth, and publish.
+  auto ring_step = [&](int i, int bb) __attribute__((always_inline)) {
+    if constexpr (kRing) {
+      ring_store(ar[i], (bb + 1) & 1);
+      ring_load(ar[i], min(bb + 1 + kDepth, nb - 1));
+      lds_barrier();
+    }
+  };
   int b = 0;
   for (; b + 2 * kDepth <= nb; b += kDepth) {
 #pragma unroll
@@ -529,6 +599,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
       consume(i, b + i);
       __builtin_amdgcn_sched_barrier(0);
       issue(i, b + i + kDepth);
+      ring_step(i, b + i);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -537,17 +608,21 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     if (b + i < nb) {
       consume(i, b + i);
       if (b + i + kDepth < nb) issue(i, b + i + kDepth);
+      if (b + i + 1 < nb) ring_step(i, b + i);
     }
   }
 #pragma unroll
   for (int i = 0; i < kDepth - 1; ++i)
-    if (b + kDepth + i < nb) consume(i, b + kDepth + i);
+    if (b + kDepth + i < nb) {
+      consume(i, b + kDepth + i);
+      if (b + kDepth + i + 1 < nb) ring_step(i, b + kDepth + i);
+    }
 
   // Wide tiles (each wave its own chunk): the wave hands off on its own.
   if constexpr (EPI == EPI_STORE && CPW == kWaves) return wave_epilogue<GROUPED, MR>(p, acc, chunk, split, 1);
 
   // ---- epilogue: accumulators -> LDS tile [mrows][256] fp32 ----
-  if constexpr (!kDirect) __syncthreads();  // every wave is done with the staged A
+  if constexpr (!kDirect && !kRing) __syncthreads();  // every wave is done with the staged A
   float* tile = reinterpret_cast<float*>(smem);
   {
 #pragma unroll
