@@ -133,9 +133,11 @@ class DecodeStep:
     17408->5120 through the SiLU-gated op on that `mixed` row -- the
     production call sequence (langburst/model.py:1414-1482).  W4 g128 random
     packed weights, all resident (about 10.9 GB).  fused_mlp: gate/up, SiLU
-    and down as one lb_marlin_mlp_fused call asking for one launch (mode 1; one launch
-    for M = 2..16, the two launches at M = 1), whose output is bit-identical
-    to the two calls."""
+    and down as one lb_marlin_mlp_fused call asking for one launch (mode 1: one
+    launch where both projections plan the same tiles as the two calls, here
+    M <= 4; the two calls otherwise), whose output is bit-identical to the two
+    calls.  A call is one op of the C ABI; the SiLU-gated down projection at
+    M >= 5 is two kernel launches (the gated activations first)."""
 
     HIDDEN, INTER, QKV, O_IN = 5120, 17408, 7168, 5120
 
@@ -160,7 +162,7 @@ class DecodeStep:
         self.down_out = torch.empty((m, h), dtype=torch.float16, device=dev)
         self.ws = torch.zeros((2 * it // 128 * 16,), dtype=torch.int32, device=dev)
         self.fused_mlp = fused_mlp
-        self.launches_per_layer = 4
+        self.calls_per_layer = 4
         if fused_mlp:
             from neurova_amd import capi
 
@@ -168,7 +170,7 @@ class DecodeStep:
             self.fws = torch.zeros((capi.marlin_mlp_fused_workspace_len(m, h, it),), dtype=torch.int32, device=dev)
             self.fscratch = torch.empty((capi.marlin_mlp_fused_scratch_bytes(m, h, it),), dtype=torch.uint8,
                                         device=dev)
-            self.launches_per_layer = 2 + capi.marlin_mlp_fused_launches(m, h, it, 128, 128, capi.MLP_ONE_LAUNCH)
+            self.calls_per_layer = 2 + capi.marlin_mlp_fused_launches(m, h, it, 128, 128, capi.MLP_ONE_LAUNCH)
         per_layer = (marlin_bytes(m, h, self.QKV) + marlin_bytes(m, self.O_IN, h) + marlin_bytes(m, h, 2 * it)
                      + marlin_bytes(m, it, h) + m * it * 2)  # the gated op reads [gate | up]: 2K halves per row
         self.bytes_per_step = per_layer * layers
@@ -189,7 +191,7 @@ class DecodeStep:
 
 
 def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5, fused_mlp=False):
-    """Graph-captured decode steps (3 or 4 launches per layer), timed with events."""
+    """Graph-captured decode steps (3 or 4 op calls per layer), timed with events."""
     ds = DecodeStep(torch, dev, m, layers, seed=100 + m, fused_mlp=fused_mlp)
     side = torch.cuda.Stream()
     side.wait_stream(torch.cuda.current_stream())
@@ -209,7 +211,7 @@ def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5, fused_mlp=False):
     stop.record(stream)
     torch.cuda.synchronize()
     us = start.elapsed_time(stop) * 1e3 / replays
-    res = {"layers": layers, "launches_per_step": ds.launches_per_layer * layers, "us_per_step": round(us, 1),
+    res = {"layers": layers, "calls_per_step": ds.calls_per_layer * layers, "us_per_step": round(us, 1),
            "bytes_per_step": ds.bytes_per_step, "weight_bytes_resident": ds.weight_bytes,
            "GB/s": round(ds.bytes_per_step / us / 1e3, 1),
            "frac_hbm": round(ds.bytes_per_step / us / 1e3 / HBM_PEAK_GBS, 4)}
@@ -602,7 +604,7 @@ def main():
         for mm in (4, 16):
             extra[f"decode_step_64_layers_m{mm}_fused_mlp"] = r = decode_step_sweep(torch, lc, dev, mm, fused_mlp=True)
             log(f"[bench] 64-layer decode step M={mm}, one-launch MLP: {r['us_per_step']:.1f} us, "
-                f"{r['launches_per_step']} launches")
+                f"{r['calls_per_step']} calls")
         result["extra"] = extra
 
     if not args.skip_cpu:
