@@ -194,6 +194,13 @@ constexpr int kLdsRows = 1;                        // rows per wave (one matrix)
 constexpr int kLdsThreads = kLdsWaves * kWave;
 constexpr int kLdsUnitBytes = 68;                  // 16 staged pair words + the unit's zero-point share
 constexpr int64_t kLdsMaxBytes = 64 * 1024;
+// Lane steps of codes prefetched before the activation staging (at most;
+// one matrix per wave, about half for two).  Measured at K = 17408 against one
+// step: 2 bits (5 steps) 10.65 -> 10.1 us, 3 bits (9 steps) 13.0 -> 12.0 us,
+// in_proj_ba (K = 5120, 4 bits, 3 steps) 3.8 -> 3.0 us; 8 bits (32 bytes per
+// lane step) 0.5 us slower with 3 or 5 steps, so it keeps one.
+constexpr int kLdsPreMax = 9;
+constexpr int kLdsPreMax8 = 1;
 
 // Pair q (0..15) of a 32-code unit: codes (lo, hi) and their bit offset.  The
 // decode below produces the pairs in this order.
@@ -280,7 +287,7 @@ __device__ __forceinline__ void decode_unit(const uint32_t* w, uint32_t (&b)[16]
 // Arguments as scalars, the ones the prologue needs first: gfx950 preloads
 // the leading 16 dwords into SGPRs at wave launch (a struct argument is not
 // preloaded), so the code prefetch below needs no kernarg fetch.
-template <int BITS, int NW, int R, int UPL>
+template <int BITS, int NW, int R, int UPL, int KPRE>
 __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t* q0, const uint8_t* q1,
                                                                   const uint16_t* s0, const uint16_t* s1,
                                                                   const uint16_t* x, int packed_cols, int scale_cols,
@@ -311,10 +318,10 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t*
       srow[a][r] = sm[a] + row * scale_cols;
     }
   constexpr int kStepWords = UPL * BITS;
-  // 2 bits: 64 bytes of codes per lane (most of a 17408-column row); wider
-  // codes one step (measured: more registers held across the staging cost
-  // more than the latency they hide)
-  constexpr int kPre = BITS == 2 ? 16 / kStepWords : 1;
+  // KPRE lane steps of codes (the host picks enough to cover the row where the
+  // registers allow): the whole row is requested at once, so no lane waits a
+  // second memory round trip for the row's last units
+  constexpr int kPre = KPRE;
   auto load_step = [&](int u0, uint32_t (&w)[NW][R][kStepWords], float (&sc)[UPL][NW][R])
       __attribute__((always_inline)) {
 #pragma unroll
@@ -521,21 +528,36 @@ int launch_lds(const Params& p, int bits, hipStream_t st) {
   // pair lies inside the row.  Measured at K = 17408: 2 bits 4 % faster; 3 bits
   // mixed (g64 faster, g128 slower); 4 bits 15 % slower, so 3-8 bits keep one.
   const bool pairs = ((p.cols >> 5) & 1) == 0;
+  // Lane steps prefetched before the staging: enough to cover the row (one
+  // flood of requests, no second round trip for the row's tail), up to
+  // kLdsPreMax, so that the workgroups of a BASELINE rowwise launch stay
+  // resident at once.
+  const int upl = (bits == 2 && pairs) ? 2 : 1;
+  const int64_t steps = ((p.cols >> 5) + upl * kWave - 1) / (upl * kWave);
+  const int cap = bits == 8 ? kLdsPreMax8 : (NW == 1 ? kLdsPreMax : 5);
+  const int64_t want = std::min<int64_t>(steps, cap);
+  const int kp = want <= 1 ? 1 : want <= 2 ? 2 : want <= 3 ? 3 : want <= 5 ? 5 : 9;
+#define LB_LAUNCH(B, U, KP)                                                                                  \
+  hipLaunchKernelGGL((rowwise_lds_kernel<B, NW, R, U, KP>), grid, dim3(kLdsThreads), lds, st, p.q[0], p.q[1],  \
+                     p.s[0], p.s[1], p.x, (int)p.packed_cols, (int)p.scale_cols, (int)p.cols, (int)p.rows,      \
+                     p.unit_shift, p.y[0], p.y[1])
+#define LB_LKP(B, U)                          \
+  do {                                        \
+    if (kp == 1) LB_LAUNCH(B, U, 1);          \
+    else if (kp == 2) LB_LAUNCH(B, U, 2);     \
+    else if (kp == 3) LB_LAUNCH(B, U, 3);     \
+    else if (kp == 5) LB_LAUNCH(B, U, 5);     \
+    else LB_LAUNCH(B, U, 9);                  \
+  } while (0)
   switch (bits) {
-#define LB_LAUNCH(B, U)                                                                                   \
-  hipLaunchKernelGGL((rowwise_lds_kernel<B, NW, R, U>), grid, dim3(kLdsThreads), lds, st, p.q[0], p.q[1], p.s[0], \
-                     p.s[1], p.x, (int)p.packed_cols, (int)p.scale_cols, (int)p.cols, (int)p.rows, p.unit_shift,    \
-                     p.y[0], p.y[1])
-#define LB_LCASE(B)            \
-  case B:                      \
-    if (pairs) LB_LAUNCH(B, 2); \
-    else LB_LAUNCH(B, 1);       \
-    break;
-    LB_LCASE(2)
-    case 3: LB_LAUNCH(3, 1); break;
-    case 4: LB_LAUNCH(4, 1); break;
-    case 8: LB_LAUNCH(8, 1); break;
-#undef LB_LCASE
+    case 2:
+      if (pairs) LB_LKP(2, 2);
+      else LB_LKP(2, 1);
+      break;
+    case 3: LB_LKP(3, 1); break;
+    case 4: LB_LKP(4, 1); break;
+    case 8: LB_LAUNCH(8, 1, kLdsPreMax8); break;
+#undef LB_LKP
 #undef LB_LAUNCH
     default: return LB_ERR_ARG;
   }
