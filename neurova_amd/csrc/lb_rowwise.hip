@@ -194,6 +194,8 @@ constexpr int kLdsRows = 1;                        // rows per wave (one matrix)
 constexpr int kLdsThreads = kLdsWaves * kWave;
 constexpr int kLdsUnitBytes = 68;                  // 16 staged pair words + the unit's zero-point share
 constexpr int64_t kLdsMaxBytes = 64 * 1024;
+// activation units staged per thread (the launch allows units * kLdsUnitBytes <= kLdsMaxBytes)
+constexpr int kStageUnits = (int)((kLdsMaxBytes / kLdsUnitBytes + kLdsThreads - 1) / kLdsThreads);
 // Lane steps of codes prefetched before the activation staging (at most;
 // one matrix per wave, about half for two).  Measured at K = 17408 against one
 // step: 2 bits (5 steps) 10.65 -> 10.1 us, 3 bits (9 steps) 13.0 -> 12.0 us,
@@ -301,8 +303,8 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t*
   constexpr int z = 1 << (BITS - 1);
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), lane = tid & 63;
 
-  // ---- the rows' first kPre lane steps of codes and scales, issued before
-  // the activation staging so that their latency overlaps it ----
+  // ---- per-row bases; the first kPre lane steps of codes and scales are
+  // issued right after the activation row's loads, before the staging ----
   const int64_t row0 = ((int64_t)blockIdx.x * kLdsWaves + wave) * R;
   const uint8_t* const qm[2] = {q0, q1};
   const uint16_t* const sm[2] = {s0, s1};
@@ -335,6 +337,18 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t*
         for (int j = 0; j < UPL; ++j) sc[j][a][r] = h2f(srow[a][r][(uint32_t)(u0 + j) >> unit_shift]);
       }
   };
+  // ---- the activation row's loads first (at most kStageUnits units per
+  // thread), then the codes, so that the staging waits only for the row and
+  // not for the code stream behind it ----
+  uint4 xl[kStageUnits][4];
+#pragma unroll
+  for (int su = 0; su < kStageUnits; ++su) {
+    const int u = min(tid + su * kLdsThreads, units - 1);
+    const uint4* xs = reinterpret_cast<const uint4*>(x + (int64_t)u * 32);
+#pragma unroll
+    for (int v = 0; v < 4; ++v) xl[su][v] = xs[v];
+  }
+  __builtin_amdgcn_sched_barrier(0);
   uint32_t wpre[kPre][NW][R][kStepWords];
   float spre[kPre][UPL][NW][R];
 #pragma unroll
@@ -343,18 +357,20 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t*
     const int u0 = min(UPL * lane + i * UPL * kWave, units - UPL);
     load_step(u0, wpre[i], spre[i]);
   }
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- stage the activation row in pair order, and each unit's z * sum(x) ----
-  for (int u = tid; u < units; u += kLdsThreads) {
-    const uint4* xs = reinterpret_cast<const uint4*>(x + (int64_t)u * 32);
+#pragma unroll
+  for (int su = 0; su < kStageUnits; ++su) {
+    const int u = tid + su * kLdsThreads;
+    if (u >= units) break;
     uint32_t xd[16];
 #pragma unroll
     for (int v = 0; v < 4; ++v) {
-      const uint4 t4 = xs[v];
-      xd[4 * v] = t4.x;
-      xd[4 * v + 1] = t4.y;
-      xd[4 * v + 2] = t4.z;
-      xd[4 * v + 3] = t4.w;
+      xd[4 * v] = xl[su][v].x;
+      xd[4 * v + 1] = xl[su][v].y;
+      xd[4 * v + 2] = xl[su][v].z;
+      xd[4 * v + 3] = xl[su][v].w;
     }
     uint32_t pw[16];
     float sx = 0.f;  // sum of the unit's activations
@@ -371,7 +387,7 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t*
     for (int v = 0; v < 4; ++v) xt[v * units + u] = (u32x4){pw[4 * v], pw[4 * v + 1], pw[4 * v + 2], pw[4 * v + 3]};
     corr[u] = (float)z * sx;
   }
-  __syncthreads();
+  lds_barrier();  // LDS only: the code loads stay in flight
 
   // ---- R rows of each of NW matrices per wave ----
   float acc[NW][R];
