@@ -452,7 +452,8 @@ def main():
     ap.add_argument("--gemm-probe", action="store_true", help="run the prefill GEMM counter probe and exit")
     ap.add_argument("--mlp-probe", action="store_true", help="time the decode MLP (two launches / one launch) and exit")
     ap.add_argument("--stream-probe", action="store_true",
-                    help="time the streaming-read ceiling over the headline's bytes and exit")
+                    help="time the streaming-read ceiling over the headline's bytes (or --stream-mb) and exit")
+    ap.add_argument("--stream-mb", default="", help="comma-separated MB (1e6 bytes) for --stream-probe")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU only (this build has no multi-GPU path); got --gpus {args.gpus}",
@@ -479,9 +480,12 @@ def main():
         mlp_probe(torch, dev)
         return
     if args.stream_probe:
-        pc = marlin_bytes(1, 5120, 17408)
-        r = stream_ceiling(torch, dev, pc, sets_for(pc), steps=max(1, args.steps // 10))
-        log(f"[stream-probe] {json.dumps(r)}")
+        sizes = [int(float(v) * 1e6) for v in args.stream_mb.split(",")] if args.stream_mb else \
+            [marlin_bytes(1, 5120, 17408)]
+        for pc in sizes:
+            r = stream_ceiling(torch, dev, pc, sets_for(pc), steps=max(1, args.steps // 10),
+                               wg_counts=(256, 512, 1024, 2048, 4096))
+            log(f"[stream-probe] {json.dumps(r)}")
         return
     use_graph = not args.no_graph
     log(f"[bench] device {torch.cuda.get_device_name(dev)}; graph={use_graph}")
