@@ -83,9 +83,13 @@ SHAPES = [
 ]
 
 
-@pytest.mark.parametrize("m", [1, 32])
+@pytest.mark.parametrize("m", [1, 5, 16, 24, 32])
 @pytest.mark.parametrize("name,k,n,silu", SHAPES)
 def test_decode_step_projection_vs_oracle(dev, name, k, n, silu, m):
+    """Every decode form at the model's shapes: staged (M = 1), direct-A tiles
+    (QKV, O and the SiLU-gated down from M = 5, the last after its gated
+    activations are formed once), the LDS ring (gate/up at M = 16, 24, 32),
+    16- and 32-row MFMA tiles (M <= 16, M = 24 and 32)."""
     print_case("decode-step shape", name, m, k, n)
     seed = 10 * [sh[0] for sh in SHAPES].index(name) + m
     qw, s, x = _inputs(m, k, n, seed=seed)
