@@ -387,9 +387,11 @@ def gemm_probe(torch, lc, dev, calls=6):
 
 def mlp_probe(torch, dev, calls=40):
     """The production MLP at the model's shape (hidden 5120, intermediate
-    17408, W4 g128) for M = 1, 4, 16: `calls` graph-replayed calls of the two
-    projections and of the one-launch kernel (lb_marlin_mlp_fused, mode 1),
-    over 4 rotating weight sets, for the kernel-trace runs."""
+    17408, W4 g128) for M = 1, 4, 16, 32: `calls` graph-replayed calls of the
+    two reference ops and of lb_marlin_mlp_fused (mode 1: one launch where its
+    tiles match the two ops', M <= 4; otherwise its two-launch form, whose
+    gate_up launch stores the gated activations), over 4 rotating weight sets,
+    for the kernel-trace runs."""
     from neurova_amd import capi
 
     h, it, sets = DecodeStep.HIDDEN, DecodeStep.INTER, 4
@@ -402,7 +404,7 @@ def mlp_probe(torch, dev, calls=40):
         return q, s
 
     w = [(tensor(h, 2 * it), tensor(it, h)) for _ in range(sets)]
-    for m in (1, 4, 16):
+    for m in (1, 4, 16, 32):
         x = torch.randn((m, h), device=dev, generator=gen).half()
         mixed = torch.empty((m, 2 * it), dtype=torch.float16, device=dev)
         out = torch.empty((m, h), dtype=torch.float16, device=dev)
@@ -430,7 +432,7 @@ def mlp_probe(torch, dev, calls=40):
             (gq, gs), (dq, ds) = w[i % sets]
             assert capi.marlin_mlp_streaming(gq, gs, dq, ds, x, out, accum, sync, h, it, 128, 128, ssc) == 0
 
-        for name, fn, n_calls in (("two launches", pair, calls), ("one launch", fused, calls),
+        for name, fn, n_calls in (("two reference ops", pair, calls), ("lb_marlin_mlp_fused mode 1", fused, calls),
                                   ("streaming (fp32 numerics)", streaming, sets)):
             ms, _, nc = time_calls(torch, fn, sets, calls_per_step_for(sets, n_calls), 1, True)
             log(f"[mlp-probe] M={m:2d} {name}: {ms * 1e3 / nc:.2f} us per MLP")

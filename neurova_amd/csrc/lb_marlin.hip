@@ -413,10 +413,11 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   // The GEMM kernel addresses A, B and s through 32-bit buffer resources.
   const int64_t a_bytes = m * k * 2 * (var == V_SILU ? 2 : 1);
   if (m > skinny::kMaxM && (a_bytes >= (1LL << 31) || k * n / 2 >= (1LL << 31))) return LB_ERR_PROB_SHAPE;
-  const Plan pl = make_plan(m, n, k, workspace_len, var == V_SILU ? gemm::A_SILU_PACKED : gemm::A_PLAIN,
-                            var == V_ARGMAX);
+  const bool gated = var == V_SILU || var == V_SILU_DONE;
+  const Plan pl = make_plan(m, n, k, workspace_len, gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, var == V_ARGMAX);
+  if (var == V_SILU_DONE && !pl.skinny) return LB_ERR_ARG;  // decode batches only
   if (workspace_len < counters_needed(pl, var == V_ARGMAX)) return LB_ERR_WORKSPACE;
-  const size_t need = pl.partial_bytes + (var == V_ARGMAX ? pl.keys_bytes : 0) + pl.act_bytes;
+  const size_t need = pl.partial_bytes + (var == V_ARGMAX ? pl.keys_bytes : 0) + (var == V_SILU ? pl.act_bytes : 0);
   if (need > 0 && (!scratch || scratch_bytes < need)) return LB_ERR_SCRATCH;
   if (need > 0 && !lbh::aligned(scratch, 16)) return LB_ERR_ALIGN;
 
@@ -481,6 +482,7 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
 #define LB_SKG(AMV, EPV) do { if (grouped) LB_SKC(AMV, EPV, true); else LB_SKC(AMV, EPV, false); } while (0)
     if (var == V_PLAIN) LB_SKG(skinny::A_PLAIN, skinny::EPI_STORE);
     else if (var == V_SILU) LB_SKG(skinny::A_SILU_PACKED, skinny::EPI_STORE);
+    else if (var == V_SILU_DONE) LB_SKG(skinny::A_PLAIN, skinny::EPI_STORE);
     else LB_SKG(skinny::A_PLAIN, skinny::EPI_ARGMAX);
 #undef LB_SKG
 #undef LB_SKC
@@ -668,8 +670,10 @@ extern "C" int lb_marlin_mlp_streaming(const int32_t* gate_up_qweight, const uin
 // ---------------------------------------------------------------------------
 namespace {
 struct FusedMlpPlan {
-  marlin::Plan up, down;  // the separate projections' tilings
+  marlin::Plan up, down;  // the one launch's staged tilings
+  marlin::Plan up2, down2;  // the tilings the two projections plan as separate calls
   bool one_launch = false;
+  bool act_path = false;  // two launches: gate_up stores fp16(silu(g) * u), no [g | u] round trip
   int wgs = 0;
   size_t lds = 0;
   size_t up_partial = 0, act = 0, down_partial = 0;  // scratch offsets
@@ -734,6 +738,11 @@ FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g
   p.down = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED, false, false);
   const marlin::Plan up2 = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN);
   const marlin::Plan down2 = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED);
+  p.up2 = up2;
+  p.down2 = down2;
+  // decode tiles of 2 or 4 chunks pair gate and up chunks; 64-column tiles
+  // (direct A at M = 17..32) and prefill tiles take the [g | u] round trip
+  p.act_path = up2.skinny && up2.cpw >= 2 && down2.skinny;
   const bool wanted = mode == kMlpOne;
   // The one launch must sum every output as the two launches do (bit-identical
   // results): only where both projections plan the same staged tiles.
@@ -837,6 +846,48 @@ extern "C" int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qwe
   unsigned char* sc = reinterpret_cast<unsigned char*>(scratch);
   hipStream_t st = (hipStream_t)stream;
   const int64_t n_up = 2 * intermediate;
+
+  if (!pl.one_launch && pl.act_path) {
+    // gate_up -> fp16(silu(g) * u) [batch][intermediate] (in the [g | u]
+    // region), then the down projection over it with the SiLU-gated op's own
+    // plan: the same sums as the two reference calls
+    uint16_t* act = reinterpret_cast<uint16_t*>(sc + pl.mixed);
+    const marlin::Plan& u2 = pl.up2;
+    skinny::Params u{};
+    u.a = x; u.b = reinterpret_cast<const uint32_t*>(gate_up_qweight); u.s = gate_up_scales; u.c = nullptr;
+    u.counters = workspace + pl.ws_up;
+    u.partial = u2.partial_bytes ? reinterpret_cast<float*>(sc + pl.up_partial) : nullptr;
+    u.m = (int)batch; u.n = (int)n_up; u.k = (int)hidden; u.splits = u2.splits;
+    u.kp_total = (int)(hidden / 32); u.n_cg = u2.n_cg;
+    u.act_out = reinterpret_cast<uint32_t*>(act);
+    u.gate_chunks = (int)(intermediate / 64);
+    const size_t lds = std::max(u2.lds, (size_t)batch * skinny::kCols * 4);
+    dim3 grid((unsigned)u2.n_cg, (unsigned)u2.splits, 1);
+#define LB_ACT(AMV, GV, CV, MRV) \
+  hipLaunchKernelGGL((mlp::mlp_gate_up_act_kernel<AMV, GV, CV, MRV>), grid, dim3(skinny::kThreads), lds, st, u)
+#define LB_ACTG(AMV, CV, MRV)                   \
+  do {                                          \
+    if (g1) LB_ACT(AMV, true, CV, MRV);         \
+    else LB_ACT(AMV, false, CV, MRV);           \
+  } while (0)
+    if (!u2.direct) {  // staged (M <= 16)
+      if (u2.cpw == 4) LB_ACTG(skinny::A_PLAIN, 4, 1);
+      else LB_ACTG(skinny::A_PLAIN, 2, 1);
+    } else if (u2.cpw == 4) {  // the LDS ring
+      if (u2.mr == 1) LB_ACTG(skinny::A_RING, 4, 1);
+      else LB_ACTG(skinny::A_RING, 4, 2);
+    } else {  // direct A, 2-chunk tiles (M <= 16)
+      LB_ACTG(skinny::A_DIRECT, 2, 1);
+    }
+#undef LB_ACTG
+#undef LB_ACT
+    const int e = lbh::launch_status();
+    if (e != LB_OK) return e;
+    const size_t rest = scratch_bytes - pl.down_partial;
+    return marlin::run(marlin::V_SILU_DONE, act, down_qweight, out, down_scales, batch, hidden, intermediate,
+                       workspace + pl.ws_down, workspace_len - pl.ws_down, down_group_size, nullptr, nullptr,
+                       sc + pl.down_partial, rest, st);
+  }
 
   if (!pl.one_launch) {
     uint16_t* mixed = reinterpret_cast<uint16_t*>(sc + pl.mixed);

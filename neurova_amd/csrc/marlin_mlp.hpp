@@ -114,5 +114,15 @@ __global__ __launch_bounds__(skinny::kThreads) void marlin_mlp_fused_kernel(Fuse
   }
 }
 
+// The two-launch form's gate_up launch for decode batches: the tiles the
+// plain gate_up projection plans (same k splits, so every g and u sums the
+// same terms in the same order), with the gate and up chunks of the same
+// neurons paired per tile, storing fp16(silu(g) * u) of the fp16 outputs
+// (skinny::EPI_ACT) for the down projection instead of [g | u].
+template <int AM, bool G, int CPW, int MR>
+__global__ __launch_bounds__(skinny::kThreads) void mlp_gate_up_act_kernel(skinny::Params p) {
+  skinny::skinny_tile<AM, skinny::EPI_ACT, G, CPW, MR>(p, blockIdx.x, blockIdx.y);
+}
+
 }  // namespace mlp
 }  // namespace lb

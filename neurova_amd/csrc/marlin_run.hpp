@@ -7,7 +7,9 @@
 namespace lb {
 namespace marlin {
 
-enum Variant { V_PLAIN = 0, V_SILU = 1, V_ARGMAX = 2 };
+// V_SILU_DONE: the SiLU-gated projection's plan and sums, with A given as the
+// gated activations fp16(silu(g) * u) [M][K] (decode batches, M <= 32).
+enum Variant { V_PLAIN = 0, V_SILU = 1, V_ARGMAX = 2, V_SILU_DONE = 3 };
 
 // Validates, plans and launches one projection on `st`; `scratch` holds the
 // split-K partials (and the argmax tile keys) the plan needs.  Returns an

@@ -148,15 +148,17 @@ __device__ __forceinline__ int tile_chunk(const Params& p, int cg, int c) {
   return cg * CPW + c;
 }
 
-// The split-K collect of a plain-store tile: sums the T shares of columns
-// [col0, col0 + 4 CQ) of every row in share order (deterministic), rounds to
-// fp16 (the per-column scale after that, as the reference does) and stores.
+// The split-K collect of a tile: sums the T shares of columns [col0, col0 +
+// 4 CQ) of every row in share order (deterministic), rounds to fp16 (the
+// per-column scale after that, as the reference does) and hands each value to
+// `store(row, column - col0, fp16 bits)` (the output, or the SiLU-gated
+// epilogue's LDS exchange).
 // Thread t (of NT) takes column quad t % CQ and rows t / CQ + (NT / CQ) i, and
 // keeps every row's loads of up to kSU shares in flight together (16-byte
 // device-coherent loads, at most kMaxLoads per thread): the collect costs one
 // memory round trip per kSU shares, not one per four rows.
-template <bool GROUPED, int CQ, int NT, int ROWS, int kMaxLoads>
-__device__ __forceinline__ void collect_store(const Params& p, int total, int col0, int t) {
+template <bool GROUPED, int CQ, int NT, int ROWS, int kMaxLoads, typename Store>
+__device__ __forceinline__ void collect_store(const Params& p, int total, int col0, int t, Store store) {
   constexpr int kRowStep = NT / CQ;
   constexpr int kRowIters = (ROWS + kRowStep - 1) / kRowStep;
   constexpr int kSU = kMaxLoads / kRowIters < 1 ? 1 : kMaxLoads / kRowIters > 8 ? 8 : kMaxLoads / kRowIters;
@@ -200,7 +202,7 @@ __device__ __forceinline__ void collect_store(const Params& p, int total, int co
       for (int e = 0; e < 4; ++e) {
         f16 h = (f16)sum[i][e];
         if (!GROUPED) h = h * cs[e];
-        p.c[(int64_t)row * p.n + ncol + e] = __builtin_bit_cast(uint16_t, h);
+        store(row, ncol - col0 + e, __builtin_bit_cast(uint16_t, h));
       }
     }
   }
@@ -287,7 +289,8 @@ __device__ __forceinline__ bool wave_epilogue(const Params& p, const f32x4 (&acc
     return true;
   }
   // (MR = 2: fewer loads in flight, so that two workgroups still fit a CU)
-  collect_store<GROUPED, 16, kWave, 16 * MR, MR == 1 ? 32 : 16>(p, total, col0, lane);
+  collect_store<GROUPED, 16, kWave, 16 * MR, MR == 1 ? 32 : 16>(
+      p, total, col0, lane, [&](int row, int col, uint16_t v) { p.c[(int64_t)row * p.n + col0 + col] = v; });
   return true;
 }
 
@@ -306,9 +309,10 @@ struct NoWait {
 template <int AM, int EPI, bool GROUPED, int CPW, int MR = 1, typename WaitA = NoWait>
 __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const int split, WaitA wait_for_a = WaitA()) {
   static_assert(EPI != EPI_ACT || CPW >= 2, "EPI_ACT pairs a gate and an up chunk");
-  static_assert(MR == 1 || ((AM == A_DIRECT || AM == A_RING) && EPI == EPI_STORE), "row blocks > 1: plain store");
+  static_assert(MR == 1 || ((AM == A_DIRECT || AM == A_RING) && (EPI == EPI_STORE || EPI == EPI_ACT)),
+                "row blocks > 1: direct or ring A, store or SiLU-gated epilogue");
   static_assert(MR >= 1 && MR <= kMaxMR, "row blocks");
-  static_assert(AM != A_RING || (CPW == kWaves && EPI == EPI_STORE), "A ring: 4-chunk plain-store tiles");
+  static_assert(AM != A_RING || (CPW == kWaves && EPI != EPI_ARGMAX), "A ring: 4-chunk tiles");
   constexpr bool kDirect = AM == A_DIRECT;
   constexpr bool kRing = AM == A_RING;
   constexpr int kRows = 16 * MR;  // rows of the MFMA tile
@@ -622,7 +626,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   if constexpr (EPI == EPI_STORE && CPW == kWaves) return wave_epilogue<GROUPED, MR>(p, acc, chunk, split, 1);
 
   // ---- epilogue: accumulators -> LDS tile [mrows][256] fp32 ----
-  if constexpr (!kDirect && !kRing) __syncthreads();  // every wave is done with the staged A
+  if constexpr (!kDirect) __syncthreads();  // every wave is done with the staged A (or the ring)
   float* tile = reinterpret_cast<float*>(smem);
   {
 #pragma unroll
@@ -653,6 +657,20 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     v[r] = t;
   }
 
+  // EPI_ACT: thread t forms neuron pair t of a row from the tile's fp16
+  // outputs [mrows][64 CPW] (gate half, then up half) in LDS, with the same
+  // SiLU-gated product as the A_SILU_PACKED staging, and publishes it.
+  auto act_pairs = [&](const uint16_t* xch) __attribute__((always_inline)) {
+    constexpr int kPairs = 16 * CPW;  // neuron pairs per row
+    const uint32_t* xw = reinterpret_cast<const uint32_t*>(xch);
+    for (int it = tid; it < mrows * kPairs; it += kThreads) {
+      const int r = it / kPairs, t2 = it - r * kPairs;
+      const uint32_t gw = xw[r * (32 * CPW) + t2];
+      const uint32_t uw = xw[r * (32 * CPW) + kPairs + t2];
+      publish(p.act_out + (int64_t)r * (p.n / 4) + (int64_t)cg * kPairs + t2, silu_mul2(gw, uw));
+    }
+  };
+
   if (p.splits > 1) {
     float* part = p.partial + (int64_t)split * p.m * p.n + n;
 #pragma unroll
@@ -666,7 +684,23 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     if (s_prev != p.splits - 1) return false;  // not the last split of this tile
     if (tid == 0) reset_counter(ctr);
     if constexpr (EPI == EPI_STORE) {  // every thread of the workgroup collects
-      collect_store<GROUPED, 16 * CPW, kThreads, kRows, 32>(p, p.splits, cg * 64 * cpw, tid);
+      const int col0 = cg * 64 * cpw;
+      collect_store<GROUPED, 16 * CPW, kThreads, kRows, 32>(
+          p, p.splits, col0, tid, [&](int row, int col, uint16_t v) { p.c[(int64_t)row * p.n + col0 + col] = v; });
+      return true;
+    }
+    if constexpr (EPI == EPI_ACT) {
+      // every thread collects, the gate half and then the up half of the tile
+      // (each a contiguous run of 32 CPW columns), into the LDS exchange
+      constexpr int h = CPW / 2;
+      uint16_t* xch = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+      for (int half = 0; half < 2; ++half)
+        collect_store<GROUPED, 16 * h, kThreads, kRows, 32>(
+            p, p.splits, tile_chunk<EPI, CPW>(p, cg, half * h) * 64, tid,
+            [&](int row, int col, uint16_t v) { xch[row * 64 * CPW + half * 64 * h + col] = v; });
+      __syncthreads();
+      act_pairs(xch);
       return true;
     }
     // Sum the partials in split order; 4 rows x 8 splits of reads in flight.
@@ -714,23 +748,15 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   }
 
   if (EPI == EPI_ACT) {
-    // The tile's fp16 outputs [mrows][64 * CPW] (gate half, then up half) go
-    // through LDS; thread t then forms neuron pair t of a row with the same
-    // SiLU-gated product as the A_SILU_PACKED staging and publishes it.
-    constexpr int kTileCols = 64 * CPW, kPairs = 16 * CPW;  // neuron pairs per row
+    // the tile's fp16 outputs go through LDS to act_pairs
+    constexpr int kTileCols = 64 * CPW;
     uint16_t* xch = reinterpret_cast<uint16_t*>(smem);
     __syncthreads();  // every thread is done with the fp32 tile
 #pragma unroll
     for (int r = 0; r < kRows; ++r)
       if (r < mrows && col_live) xch[r * kTileCols + tid] = outh[r];
     __syncthreads();
-    const uint32_t* xw = reinterpret_cast<const uint32_t*>(xch);
-    for (int it = tid; it < mrows * kPairs; it += kThreads) {
-      const int r = it / kPairs, t = it - r * kPairs;
-      const uint32_t gw = xw[r * (kTileCols / 2) + t];
-      const uint32_t uw = xw[r * (kTileCols / 2) + kPairs + t];
-      publish(p.act_out + (int64_t)r * (p.n / 4) + (int64_t)cg * kPairs + t, silu_mul2(gw, uw));
-    }
+    act_pairs(xch);
     return true;
   }
 

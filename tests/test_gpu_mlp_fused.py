@@ -115,14 +115,15 @@ def test_fused_mlp_vs_two_launches_and_oracle(dev, hidden, inter, batch, gg, dg)
     assert_close_f16(got, O.marlin_gemm_silu_packed(mixed, d_q, d_s, inter, dg), what="down(silu)")
 
 
-@pytest.mark.parametrize("batch", [1, 4, 16])
+@pytest.mark.parametrize("batch", [1, 4, 16, 24, 32])
 def test_fused_mlp_model_shape_one_launch(dev, batch):
     from neurova_amd import capi
 
     launches = capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128, capi.MLP_ONE_LAUNCH)
     print_case("mlp_fused_model", batch, "launches", launches)
-    # batch 16: the two launches take direct-A tiles the one-launch kernel does
-    # not have, so mode 1 runs them too (the output stays bit-identical)
+    # from batch 5: the two launches take direct-A and ring tiles the one-launch
+    # kernel does not have, so mode 1 runs them too (the gate_up launch storing
+    # the gated activations; the output stays bit-identical)
     assert launches == (1 if batch <= 4 else 2)
     # auto: always the two launches (the one launch is opt-in)
     assert capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128) == 2
@@ -188,7 +189,7 @@ def _sample_cols(n, count, seed):
     return [(64 * c, 64 * c + 64) for c in chunks]
 
 
-@pytest.mark.parametrize("batch", [1, 4, 16])
+@pytest.mark.parametrize("batch", [1, 4, 16, 32])
 def test_fused_mlp_model_shape_vs_oracle(dev, batch):
     """The one-launch MLP at the model's shape (hidden 5120, intermediate
     17408, g128) against the oracle, column-sampled: the gate_up stage on 16
