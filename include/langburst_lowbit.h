@@ -106,11 +106,26 @@ int lb_lowbit_row_dequant(const uint8_t* qweight, int64_t rows, int64_t packed_c
 /* Bytes of scratch the Marlin entry points need for this problem. */
 size_t lb_marlin_scratch_bytes(int64_t prob_m, int64_t prob_n, int64_t prob_k, int64_t groupsize);
 
+/* The plan a Marlin entry point makes for this problem (no counterpart in the
+ * reference; for tests and tools, no device work).  variant: 0 lb_marlin_gemm,
+ * 1 lb_marlin_gemm_silu_packed, 2 lb_marlin_gemm_argmax; workspace_len as the
+ * call would pass it.  Fills out[10]:
+ *   [0] form: 0 decode tiles with the A slice staged whole, 1 decode tiles
+ *       with A fragments loaded per step, 2 decode tiles with A through an
+ *       LDS ring, 3 prefill GEMM tiles;
+ *   [1] decode: 64-column chunks per workgroup; prefill: 16-row blocks;
+ *   [2] decode: k splits of every column tile; prefill: k splits of the tail tiles;
+ *   [3] decode: 16-row MFMA blocks; prefill: whole tiles;
+ *   [4] workgroups; [5] dynamic LDS bytes per workgroup; [6] scratch bytes;
+ *   [7] workspace entries used; [8] kernel launches; [9] compute units planned for.
+ * Returns LB_OK, or the status the entry point would return for the shape. */
+int lb_marlin_describe_plan(int64_t prob_m, int64_t prob_n, int64_t prob_k, int64_t groupsize, int32_t variant,
+                            int64_t workspace_len, int64_t* out);
+
 /* C[M, N] = A[M, K] @ dequant(B), fp32 accumulate, fp16 C.  Grouped scales:
- * for M <= 16 each group's fp32 sum of x * (q - 8) is multiplied by the scale
- * once; for M > 16 the fp16 weights fp16((q - 8) * s) are accumulated, as the
- * reference does for every M.  Per-column scales: fp16(sum) * s, as the
- * reference.  Both stay within the reference tolerance.
+ * the fp16 weights fp16(fp16(q - 8) * s) are accumulated, as the reference
+ * does; per-column scales: fp16(sum of x * (q - 8)) * s, as the reference.
+ * Results differ from the reference's only by fp32 summation order.
  * Replaces marlin_cuda (csrc/marlin_cuda_kernel.cu:917-1005) as called by
  * run_lowbit_marlin_gemm (csrc/langburst_ext.cpp:67-114). */
 int lb_marlin_gemm(const uint16_t* A, const int32_t* B, uint16_t* C, const uint16_t* s,

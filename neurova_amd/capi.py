@@ -40,6 +40,7 @@ _SIGNATURES = {
     "lb_lowbit_gemm": ([P, I64, I64, P, I64, P, I64, I64, P, I64, I64, I64, I64, P], ctypes.c_int),
     "lb_lowbit_row_dequant": ([P, I64, I64, P, I64, P, P, I64, I64, I64, P], ctypes.c_int),
     "lb_marlin_scratch_bytes": ([I64, I64, I64, I64], SZ),
+    "lb_marlin_describe_plan": ([I64, I64, I64, I64, ctypes.c_int32, I64, P], ctypes.c_int),
     "lb_marlin_gemm": ([P, P, P, P, I64, I64, I64, P, I64, I64, P, SZ, P], ctypes.c_int),
     "lb_marlin_gemm_silu_packed": ([P, P, P, P, I64, I64, I64, P, I64, I64, P, SZ, P], ctypes.c_int),
     "lb_marlin_gemm_argmax": ([P, P, P, I64, I64, I64, P, I64, I64, P, P, P, I32, P, SZ, P], ctypes.c_int),
@@ -118,6 +119,24 @@ def lowbit_row_dequant(qweight, scales, row, out, cols, group_size, bits) -> int
 
 def marlin_scratch_bytes(m, n, k, group_size) -> int:
     return int(lib().lb_marlin_scratch_bytes(m, n, k, group_size))
+
+
+PLAN_FIELDS = ("form", "chunks_or_row_blocks", "splits", "row_blocks_or_full_tiles", "workgroups", "lds_bytes",
+               "scratch_bytes", "workspace_entries", "launches", "cus")
+PLAN_FORMS = ("staged", "direct", "ring", "prefill")
+
+
+def marlin_describe_plan(m, n, k, group_size, variant=0, workspace_len=None) -> dict:
+    """The plan lb_marlin_gemm (variant 0), the SiLU-gated op (1) or the argmax
+    op (2) makes for this problem; no device work.  Raises on a rejected shape."""
+    out = (ctypes.c_int64 * 10)()
+    ws = n // 128 * 16 if workspace_len is None else workspace_len
+    st = lib().lb_marlin_describe_plan(m, n, k, group_size, variant, ws, ctypes.cast(out, ctypes.c_void_p))
+    if st != LB_OK:
+        raise ValueError(f"lb_marlin_describe_plan: {status_string(st)}")
+    d = dict(zip(PLAN_FIELDS, (int(v) for v in out)))
+    d["form"] = PLAN_FORMS[d["form"]]
+    return d
 
 
 def marlin_gemm(a, b, c, s, workspace, group_size, scratch=None) -> int:

@@ -222,7 +222,6 @@ inline int skinny_splits(int64_t m, int64_t n, int64_t k, int64_t workspace_len,
   const int n_cg = (int)(n / (64 * cpw));
   const int ksub = skinny::kWaves / cpw;
   const int groups = (int)(k / 128);
-  const size_t x_all = (size_t)k * (size_t)m * 2;
   // split counters: one per chunk for wide tiles (each wave hands off on its
   // own), one per tile otherwise
   const bool can_split = workspace_len >= 1 + (cpw == skinny::kWaves ? n / 64 : (int64_t)n_cg);
@@ -234,7 +233,9 @@ inline int skinny_splits(int64_t m, int64_t n, int64_t k, int64_t workspace_len,
   const int s_traffic = (int)std::max<int64_t>(1, k / (32 * m));
   if (s > s_traffic) s = s_traffic;
   // the decode kernel stages its whole A slice in LDS
-  const int s_lds = direct ? 1 : (int)((x_all + kSkinnyMaxX - 1) / kSkinnyMaxX);
+  // (whole scale groups: at most kSkinnyMaxX / (256 M) groups per split)
+  const int64_t lds_groups = std::max<int64_t>(1, (int64_t)kSkinnyMaxX / (256 * m));
+  const int s_lds = direct ? 1 : (int)((groups + lds_groups - 1) / lds_groups);
   if (s < s_lds) s = s_lds;
   if (s > groups / ksub) s = groups / ksub;  // every wave at least one group
   if (s > 256) s = 256;  // the kernel's split arithmetic is 32-bit: groups * S < 2^32
@@ -556,6 +557,39 @@ extern "C" size_t lb_marlin_scratch_bytes(int64_t prob_m, int64_t prob_n, int64_
   const marlin::Plan c = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN, true);
   return std::max(std::max(a.partial_bytes + a.keys_bytes, b.partial_bytes + b.keys_bytes + b.act_bytes),
                   c.partial_bytes + c.keys_bytes);
+}
+
+extern "C" int lb_marlin_describe_plan(int64_t prob_m, int64_t prob_n, int64_t prob_k, int64_t groupsize,
+                                       int32_t variant, int64_t workspace_len, int64_t* out) {
+  if (!out || variant < 0 || variant > 2 || prob_m < 0 || prob_n < 0 || prob_k < 0) return LB_ERR_ARG;
+  if (prob_n % 256 != 0 || prob_k % 128 != 0) return LB_ERR_PROB_SHAPE;
+  int grouped = 0;
+  if (marlin::normalize_group(groupsize, prob_k, grouped) != LB_OK) return LB_ERR_PROB_SHAPE;
+  for (int i = 0; i < 10; ++i) out[i] = 0;
+  if (prob_m == 0 || prob_n == 0 || prob_k == 0) return LB_OK;
+  const bool argmax = variant == 2, gated = variant == 1;
+  const marlin::Plan pl = marlin::make_plan(prob_m, prob_n, prob_k, workspace_len,
+                                            gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, argmax);
+  if (pl.skinny) {
+    out[0] = !pl.direct ? 0 : pl.cpw == skinny::kWaves ? 2 : 1;
+    out[1] = pl.cpw;
+    out[2] = pl.splits;
+    out[3] = pl.mr;
+    out[4] = (int64_t)pl.n_cg * pl.splits;
+    out[5] = (int64_t)pl.lds;
+  } else {
+    out[0] = 3;
+    out[1] = pl.mb;
+    out[2] = pl.tail_splits;
+    out[3] = pl.full_tiles;
+    out[4] = pl.wgs;
+    out[5] = 0;
+  }
+  out[6] = (int64_t)(pl.partial_bytes + (argmax ? pl.keys_bytes : 0) + (gated ? pl.act_bytes : 0));
+  out[7] = marlin::counters_needed(pl, argmax);
+  out[8] = (gated && pl.direct) ? 2 : 1;
+  out[9] = marlin::device_cus();
+  return LB_OK;
 }
 
 extern "C" int lb_marlin_gemm(const uint16_t* A, const int32_t* B, uint16_t* C, const uint16_t* s,
