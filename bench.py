@@ -81,15 +81,24 @@ class RowwiseProblem:
         lc.lowbit_gemv(self.q[i], self.s[i], self.x, self.k, self.g, self.bits)
 
 
+WARM_MS = 30.0  # minimum untimed work before a timed region (graph replays)
+
+
 def time_calls(torch, fn, n_sets, steps, warmup, use_graph=True):
     """Times `steps` steps of one call per weight set (`n_sets` calls each);
     returns (elapsed_ms, steps, calls).
 
-    With use_graph the calls of one step are captured once in a HIP graph and
-    replayed; events bracket the replays on the launch stream."""
+    With use_graph the calls of `chunk` consecutive steps (the largest divisor
+    of `steps` up to 100) are captured once in a HIP graph, as a serving loop
+    captures its launches, and the graph is replayed steps / chunk times, so
+    the timed region holds exactly `steps` steps and the host-side cost of a
+    graph launch falls once per chunk rather than once per step; events
+    bracket the replays on the launch stream.  At least `warmup` untimed steps
+    (whole replays) and at least WARM_MS of untimed work run first."""
     steps = max(1, int(steps))
     stream = torch.cuda.current_stream()
     if use_graph:
+        chunk = max(d for d in range(1, min(steps, 100) + 1) if steps % d == 0)
         side = torch.cuda.Stream()
         side.wait_stream(stream)
         with torch.cuda.stream(side):
@@ -100,13 +109,35 @@ def time_calls(torch, fn, n_sets, steps, warmup, use_graph=True):
         graph = torch.cuda.CUDAGraph()
         # capture on the warmed-up stream: its per-stream buffers already exist
         with torch.cuda.graph(graph, stream=side):
-            for i in range(n_sets):
-                fn(i)
-        run_step = graph.replay
-    else:
-        def run_step():
-            for i in range(n_sets):
-                fn(i)
+            for _ in range(chunk):
+                for i in range(n_sets):
+                    fn(i)
+        replays = steps // chunk
+        # warm-up: at least `warmup` steps and at least WARM_MS of work, so the
+        # timed region starts at the engine clock a continuous decode loop runs
+        # at (the clock rises over the first ~10-20 ms of back-to-back launches)
+        warm_replays = max(1, math.ceil(max(1, int(warmup)) / chunk))
+        t0 = time.perf_counter()
+        for _ in range(warm_replays):
+            graph.replay()
+        torch.cuda.synchronize()
+        per_replay = (time.perf_counter() - t0) / warm_replays
+        extra = max(0, math.ceil(WARM_MS * 1e-3 / max(per_replay, 1e-6)) - warm_replays)
+        for _ in range(min(extra, 10000)):
+            graph.replay()
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        stop = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for _ in range(replays):
+            graph.replay()
+        stop.record(stream)
+        torch.cuda.synchronize()
+        return start.elapsed_time(stop), steps, steps * n_sets
+
+    def run_step():
+        for i in range(n_sets):
+            fn(i)
     for _ in range(max(1, int(warmup))):
         run_step()
     torch.cuda.synchronize()
@@ -201,7 +232,12 @@ def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5, fused_mlp=False):
     graph = torch.cuda.CUDAGraph()
     with torch.cuda.graph(graph, stream=side):
         ds.step(lc)
+    t0 = time.perf_counter()
     graph.replay()
+    torch.cuda.synchronize()
+    # untimed warm-up of at least WARM_MS, as in time_calls
+    for _ in range(min(100, max(0, math.ceil(WARM_MS * 1e-3 / max(time.perf_counter() - t0, 1e-6)) - 1))):
+        graph.replay()
     torch.cuda.synchronize()
     stream = torch.cuda.current_stream()
     start, stop = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
@@ -530,7 +566,9 @@ def main():
                      "traffic_source": f"{TRAFFIC_FILE} (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE per dispatch, "
                                        "calibrated on a copy kernel; not measured in this run)",
                      "bytes_per_launch": per_call, "us_per_launch": round(us_per, 3),
-                     "timing": "HIP events on the launch stream around the graph replays"},
+                     "timing": ("HIP events on the launch stream around the graph replays (graphs of up to 100 "
+                                "steps); untimed warm-up of at least the requested steps and "
+                                f"{WARM_MS:.0f} ms of work before it")},
     }
 
     if not args.skip_extra:
