@@ -182,19 +182,7 @@ constexpr int kGemmMaxTailSplits = 16;
 constexpr int kSkinnyMaxSplits = 8;  // decode: beyond this, narrower tiles instead
 constexpr size_t kSkinnyMaxX = 48 * 1024;
 
-// Compute units of the current device (cached per device; 256 on a full MI355X,
-// fewer in a compute-partitioned mode).
-inline int device_cus() {
-  static int cache[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  int v = __atomic_load_n(&cache[dev], __ATOMIC_RELAXED);
-  if (v <= 0) {
-    if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v <= 0) v = 256;
-    __atomic_store_n(&cache[dev], v, __ATOMIC_RELAXED);
-  }
-  return v;
-}
+using lbh::device_cus;
 
 // GEMM tail split: the tiles left after the last full round of resident
 // workgroups are split over K.  S minimises the tail's length in tile times,

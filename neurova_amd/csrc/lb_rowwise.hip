@@ -189,13 +189,13 @@ __global__ __launch_bounds__(kThreads) void rowwise_fast_kernel(Params p) {
 // arithmetic results below 2^-14 are flushed to zero here.)  Each wave
 // computes R rows (of NW matrices) from one LDS read of the activations.
 // ---------------------------------------------------------------------------
-constexpr int kLdsWaves = 8;                       // waves (rows x R) per workgroup
+constexpr int kLdsWaves = 8;                       // waves (rows x R) per workgroup, unless the shape below says otherwise
 constexpr int kLdsRows = 1;                        // rows per wave (one matrix)
-constexpr int kLdsThreads = kLdsWaves * kWave;
 constexpr int kLdsUnitBytes = 68;                  // 16 staged pair words + the unit's zero-point share
 constexpr int64_t kLdsMaxBytes = 64 * 1024;
-// activation units staged per thread (the launch allows units * kLdsUnitBytes <= kLdsMaxBytes)
-constexpr int kStageUnits = (int)((kLdsMaxBytes / kLdsUnitBytes + kLdsThreads - 1) / kLdsThreads);
+// activation units staged per thread of a workgroup of `threads` (the launch
+// allows units * kLdsUnitBytes <= kLdsMaxBytes)
+constexpr int stage_units(int threads) { return (int)((kLdsMaxBytes / kLdsUnitBytes + threads - 1) / threads); }
 // Lane steps of codes prefetched before the activation staging (at most;
 // one matrix per wave, about half for two).  Measured at K = 17408 against one
 // step: 2 bits (5 steps) 10.65 -> 10.1 us, 3 bits (9 steps) 13.0 -> 12.0 us,
@@ -289,13 +289,15 @@ __device__ __forceinline__ void decode_unit(const uint32_t* w, uint32_t (&b)[16]
 // Arguments as scalars, the ones the prologue needs first: gfx950 preloads
 // the leading 16 dwords into SGPRs at wave launch (a struct argument is not
 // preloaded), so the code prefetch below needs no kernarg fetch.
-template <int BITS, int NW, int R, int UPL, int KPRE>
-__global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t* q0, const uint8_t* q1,
+template <int BITS, int NW, int R, int UPL, int KPRE, int W>
+__global__ __launch_bounds__(W * kWave) void rowwise_lds_kernel(const uint8_t* q0, const uint8_t* q1,
                                                                   const uint16_t* s0, const uint16_t* s1,
                                                                   const uint16_t* x, int packed_cols, int scale_cols,
                                                                   int cols, int rows, int unit_shift, uint16_t* y0,
                                                                   uint16_t* y1) {
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
+  constexpr int kThreadsWG = W * kWave;
+  constexpr int kStageUnits = stage_units(kThreadsWG);
   const int units = cols >> 5;
   u32x4* xt = reinterpret_cast<u32x4*>(smem);                           // [4][units] pair words
   float* corr = reinterpret_cast<float*>(smem + (size_t)units * 64);    // [units]
@@ -305,7 +307,7 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t*
 
   // ---- per-row bases; the first kPre lane steps of codes and scales are
   // issued right after the activation row's loads, before the staging ----
-  const int64_t row0 = ((int64_t)blockIdx.x * kLdsWaves + wave) * R;
+  const int64_t row0 = ((int64_t)blockIdx.x * W + wave) * R;
   const uint8_t* const qm[2] = {q0, q1};
   const uint16_t* const sm[2] = {s0, s1};
   // per-row bases, wave-uniform; 32-bit offsets from them in the loop
@@ -343,7 +345,7 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t*
   uint4 xl[kStageUnits][4];
 #pragma unroll
   for (int su = 0; su < kStageUnits; ++su) {
-    const int u = min(tid + su * kLdsThreads, units - 1);
+    const int u = min(tid + su * kThreadsWG, units - 1);
     const uint4* xs = reinterpret_cast<const uint4*>(x + (int64_t)u * 32);
 #pragma unroll
     for (int v = 0; v < 4; ++v) xl[su][v] = xs[v];
@@ -362,7 +364,7 @@ __global__ __launch_bounds__(kLdsThreads) void rowwise_lds_kernel(const uint8_t*
   // ---- stage the activation row in pair order, and each unit's z * sum(x) ----
 #pragma unroll
   for (int su = 0; su < kStageUnits; ++su) {
-    const int u = tid + su * kLdsThreads;
+    const int u = tid + su * kThreadsWG;
     if (u >= units) break;
     uint32_t xd[16];
 #pragma unroll
@@ -535,9 +537,10 @@ int launch_bt(const Params& p, int bits, bool fast, hipStream_t st) {
   return lbh::launch_status();
 }
 
-template <int NW, int R>
-int launch_lds(const Params& p, int bits, hipStream_t st) {
-  const int64_t rows_per_wg = (int64_t)kLdsWaves * R;
+// One bit width of the one-row kernel on workgroups of W waves of R rows.
+template <int B, int NW, int W, int R>
+int launch_lds_bits(const Params& p, hipStream_t st) {
+  const int64_t rows_per_wg = (int64_t)W * R;
   dim3 grid((unsigned)((p.rows + rows_per_wg - 1) / rows_per_wg));
   const size_t lds = (size_t)(p.cols >> 5) * kLdsUnitBytes;
   // 2 bits: two units per lane step (16-byte code loads) where every lane's
@@ -548,36 +551,60 @@ int launch_lds(const Params& p, int bits, hipStream_t st) {
   // flood of requests, no second round trip for the row's tail), up to
   // kLdsPreMax, so that the workgroups of a BASELINE rowwise launch stay
   // resident at once.
-  const int upl = (bits == 2 && pairs) ? 2 : 1;
+  const int upl = (B == 2 && pairs) ? 2 : 1;
   const int64_t steps = ((p.cols >> 5) + upl * kWave - 1) / (upl * kWave);
-  const int cap = bits == 8 ? kLdsPreMax8 : (NW == 1 ? kLdsPreMax : 5);
+  const int cap = B == 8 ? kLdsPreMax8 : (NW == 1 ? kLdsPreMax : 5);
   const int64_t want = std::min<int64_t>(steps, cap);
   const int kp = want <= 1 ? 1 : want <= 2 ? 2 : want <= 3 ? 3 : want <= 5 ? 5 : 9;
-#define LB_LAUNCH(B, U, KP)                                                                                  \
-  hipLaunchKernelGGL((rowwise_lds_kernel<B, NW, R, U, KP>), grid, dim3(kLdsThreads), lds, st, p.q[0], p.q[1],  \
+#define LB_LAUNCH(U, KP)                                                                                     \
+  hipLaunchKernelGGL((rowwise_lds_kernel<B, NW, R, U, KP, W>), grid, dim3(W * kWave), lds, st, p.q[0], p.q[1], \
                      p.s[0], p.s[1], p.x, (int)p.packed_cols, (int)p.scale_cols, (int)p.cols, (int)p.rows,      \
                      p.unit_shift, p.y[0], p.y[1])
-#define LB_LKP(B, U)                          \
-  do {                                        \
-    if (kp == 1) LB_LAUNCH(B, U, 1);          \
-    else if (kp == 2) LB_LAUNCH(B, U, 2);     \
-    else if (kp == 3) LB_LAUNCH(B, U, 3);     \
-    else if (kp == 5) LB_LAUNCH(B, U, 5);     \
-    else LB_LAUNCH(B, U, 9);                  \
+#define LB_LKP(U)                          \
+  do {                                     \
+    if (kp == 1) LB_LAUNCH(U, 1);          \
+    else if (kp == 2) LB_LAUNCH(U, 2);     \
+    else if (kp == 3) LB_LAUNCH(U, 3);     \
+    else if (kp == 5) LB_LAUNCH(U, 5);     \
+    else LB_LAUNCH(U, 9);                  \
   } while (0)
-  switch (bits) {
-    case 2:
-      if (pairs) LB_LKP(2, 2);
-      else LB_LKP(2, 1);
-      break;
-    case 3: LB_LKP(3, 1); break;
-    case 4: LB_LKP(4, 1); break;
-    case 8: LB_LAUNCH(8, 1, kLdsPreMax8); break;
+  if constexpr (B == 8) {
+    LB_LAUNCH(1, kLdsPreMax8);
+  } else if constexpr (B == 2) {
+    if (pairs) LB_LKP(2);
+    else LB_LKP(1);
+  } else {
+    LB_LKP(1);
+  }
 #undef LB_LKP
 #undef LB_LAUNCH
+  return lbh::launch_status();
+}
+
+// Workgroup shape of the one-row kernel.  A workgroup stages the whole
+// activation row in LDS, so fewer, wider workgroups stage it fewer times;
+// the shapes below give the BASELINE configs one workgroup per CU where that
+// measured faster (one process, graph replay, against 8 waves of one row):
+//   8 bits, 5120 x 17408:  10 waves of 2 rows (256 workgroups) 18.5 us against 21.2 us;
+//   4 bits, 4096 x 4096:   16 waves of 1 row  (256 workgroups)  3.66 us against 3.95 us.
+// 2 and 3 bits keep 8 waves of one row (2.5 workgroups per CU): every other
+// shape measured slower there (10 waves of 1 or 2 rows by 11-15 %, 16 waves by
+// 25-30 %, 8 waves of 2 rows by 27-38 %).
+template <int NW>
+int launch_lds(const Params& p, int bits, hipStream_t st) {
+  if constexpr (NW == 1) {
+    const int64_t cus = lbh::device_cus();
+    if (bits == 8 && p.rows >= 20 * cus) return launch_lds_bits<8, 1, 10, 2>(p, st);
+    if (bits == 4 && p.rows >= 16 * cus) return launch_lds_bits<4, 1, 16, 1>(p, st);
+  }
+  constexpr int R = NW == 1 ? kLdsRows : (kLdsRows + 1) / 2;
+  switch (bits) {
+    case 2: return launch_lds_bits<2, NW, kLdsWaves, R>(p, st);
+    case 3: return launch_lds_bits<3, NW, kLdsWaves, R>(p, st);
+    case 4: return launch_lds_bits<4, NW, kLdsWaves, R>(p, st);
+    case 8: return launch_lds_bits<8, NW, kLdsWaves, R>(p, st);
     default: return LB_ERR_ARG;
   }
-  return lbh::launch_status();
 }
 
 int launch(Params p, int nw, int bits, hipStream_t st) {
@@ -593,7 +620,7 @@ int launch(Params p, int nw, int bits, hipStream_t st) {
     p.unit_shift = 0;
     while ((int64_t(1) << p.unit_shift) < gu) ++p.unit_shift;
   }
-  if (lds) return nw == 1 ? launch_lds<1, kLdsRows>(p, bits, st) : launch_lds<2, (kLdsRows + 1) / 2>(p, bits, st);
+  if (lds) return nw == 1 ? launch_lds<1>(p, bits, st) : launch_lds<2>(p, bits, st);
   if (p.batch <= 1) {
     return nw == 1 ? launch_bt<1, 1>(p, bits, fast, st) : launch_bt<2, 1>(p, bits, fast, st);
   }

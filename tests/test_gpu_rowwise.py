@@ -167,6 +167,18 @@ def test_cfg1_full_size(dev):
     assert exact > 0.95
 
 
+@pytest.mark.parametrize("bits,rows,cols", [(8, 5127, 2048), (8, 5140, 1056), (4, 4101, 1024), (4, 4096, 2048)])
+def test_wide_workgroup_shapes_vs_oracle(dev, bits, rows, cols):
+    """Row counts of at least 20 (8 bits) or 16 (4 bits) rows per CU take the
+    one-row kernel on 10-wave workgroups of two rows per wave or on 16-wave
+    workgroups; ragged counts leave the last workgroup partly empty."""
+    print_case("wide workgroups", bits, rows, cols)
+    _, packed, scales, x = O.make_rowwise_inputs(rows, cols, bits, 128, seed=rows)
+    got = _gemv(dev, packed, scales, x[0], cols, 128, bits)
+    exact = assert_close_f16(got, O.rowwise_gemv(packed, scales, x[0], cols, 128, bits), what=f"b{bits} {rows}x{cols}")
+    assert exact > 0.95
+
+
 @pytest.mark.parametrize("bits", [2, 3, 8])
 @pytest.mark.parametrize("group", [64, 128])
 def test_cfg4_full_size(dev, bits, group):
