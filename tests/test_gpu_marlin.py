@@ -175,6 +175,20 @@ def test_gemm_vs_oracle(dev, m):
         assert exact > 0.95
 
 
+@pytest.mark.parametrize("m,k,n,group", [(40, 8192, 1024, 128), (64, 17408, 1280, -1), (100, 4096, 2048, 128)])
+def test_gemm_split_collect_vs_oracle(dev, m, k, n, group):
+    """Prefill tiles below 128 rows split many ways over K: the last arrival
+    of a tile reads every split (its own included) in batches and sums them
+    in split order; both scale modes, repeated launches bit-identical."""
+    print_case("gemm-collect", m, k, n, group)
+    codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=2100 + m)
+    got = _run_gemm(dev, x, qw, sp, group)
+    exact = assert_close_f16(got, O.marlin_gemm(x, qw, sp, group), what=f"gemm-collect m={m} k={k} n={n} g={group}")
+    assert exact > 0.9
+    again = _run_gemm(dev, x, qw, sp, group)
+    assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
+
+
 @pytest.mark.parametrize("m", [1, 4, 16, 32])
 def test_decode_shape_cfg2(dev, m):
     """M in {1,4,16}, K=5120, N=17408, g=128 (and configs[4]'s M=32)."""
