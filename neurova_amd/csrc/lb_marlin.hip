@@ -185,16 +185,20 @@ constexpr size_t kSkinnyMaxX = 48 * 1024;
 using lbh::device_cus;
 
 // GEMM tail split: the tiles left after the last full round of resident
-// workgroups are split over K.  S minimises the tail's length in tile times,
-// ceil(T*S / slots) / S, plus a small charge per extra split for the partials
-// written and summed (about 6% of a tile time each, measured).
+// workgroups are split over K.  S minimises the tail's length in scale-group
+// times, ceil(T*S / slots) * ceil(G / S), plus a charge per extra split for the
+// partials written and summed by the last arrival, about kGemmSplitCharge
+// group times each, which does not grow with K (fitted to M = 2048 sweeps of
+// S = 2..12: K = 5120, N = 17408 runs fastest at S = 3, 290 against 294 us at
+// S = 4; K = 17408, N = 5120 at S = 3, 309.5 against 318 us at S = 4).
+constexpr int kGemmSplitCharge = 5;
 inline int choose_tail_splits(int64_t tail, int64_t slots, int groups) {
   int best = 1;
-  double best_cost = 1.0;
+  int64_t best_cost = groups;
   for (int s = 2; s <= kGemmMaxTailSplits && s <= groups; ++s) {
-    const double rounds = (double)((tail * s + slots - 1) / slots);
-    const double cost = rounds / s + 0.06 * (s - 1);
-    if (cost < best_cost - 1e-9) {
+    const int64_t rounds = (tail * s + slots - 1) / slots;
+    const int64_t cost = rounds * ((groups + s - 1) / s) + (int64_t)kGemmSplitCharge * (s - 1);
+    if (cost < best_cost) {
       best_cost = cost;
       best = s;
     }

@@ -87,7 +87,7 @@ def test_plan_rules_at_baseline_shapes(L):
     assert _plan(33, 7168, 5120)["form"] == "prefill"
     # prefill (cfg3): 128-row tiles, tail tiles split over K
     g = _plan(2048, 17408, 5120)
-    assert (g["form"], g["chunks_or_row_blocks"], g["row_blocks_or_full_tiles"], g["splits"]) == ("prefill", 8, 1024, 4)
+    assert (g["form"], g["chunks_or_row_blocks"], g["row_blocks_or_full_tiles"], g["splits"]) == ("prefill", 8, 1024, 3)
     g2 = _plan(2048, 5120, 17408)
     assert (g2["form"], g2["row_blocks_or_full_tiles"], g2["splits"], g2["workgroups"]) == ("prefill", 0, 3, 960)
     # lm_head argmax (N = 248320): staged tiles, one split
