@@ -187,17 +187,18 @@ using lbh::device_cus;
 // GEMM tail split: the tiles left after the last full round of resident
 // workgroups are split over K.  S minimises the tail's length in scale-group
 // times, ceil(T*S / slots) * ceil(G / S), plus a charge per extra split for the
-// partials written and summed by the last arrival, about kGemmSplitCharge
-// group times each, which does not grow with K (fitted to M = 2048 sweeps of
-// S = 2..12: K = 5120, N = 17408 runs fastest at S = 3, 290 against 294 us at
-// S = 4; K = 17408, N = 5120 at S = 3, 309.5 against 318 us at S = 4).
+// partials written and summed by the last arrival: about kGemmSplitCharge
+// group times for a 128-row tile (MB = 8), in proportion to the tile's rows,
+// and not growing with K (fitted to M = 2048 sweeps of S = 2..12: K = 5120,
+// N = 17408 runs fastest at S = 3, 290 against 294 us at S = 4; K = 17408,
+// N = 5120 at S = 3, 309.5 against 318 us at S = 4).
 constexpr int kGemmSplitCharge = 5;
-inline int choose_tail_splits(int64_t tail, int64_t slots, int groups) {
+inline int choose_tail_splits(int64_t tail, int64_t slots, int groups, int mb) {
   int best = 1;
-  int64_t best_cost = groups;
+  int64_t best_cost = 8 * (int64_t)groups;  // in eighths of a group time
   for (int s = 2; s <= kGemmMaxTailSplits && s <= groups; ++s) {
     const int64_t rounds = (tail * s + slots - 1) / slots;
-    const int64_t cost = rounds * ((groups + s - 1) / s) + (int64_t)kGemmSplitCharge * (s - 1);
+    const int64_t cost = 8 * rounds * ((groups + s - 1) / s) + (int64_t)kGemmSplitCharge * mb * (s - 1);
     if (cost < best_cost) {
       best_cost = cost;
       best = s;
@@ -341,7 +342,7 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
     const int64_t slots = (int64_t)gemm::wgs_per_cu(pl.mb, am) * device_cus();
     int64_t full = (tiles / slots) * slots;
     int64_t tail = tiles - full;
-    int s = tail > 0 ? choose_tail_splits(tail, slots, groups) : 1;
+    int s = tail > 0 ? choose_tail_splits(tail, slots, groups, pl.mb) : 1;
     // Few rows: the kernel streams B and is bound by bandwidth, not by the
     // MFMAs the cost model above prices; split further so that every CU gets
     // a workgroup, as long as the fp32 partials (written and read once) stay
