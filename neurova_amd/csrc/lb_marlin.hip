@@ -430,12 +430,12 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
                          (int)m, (int)k);
       av = act;
     }
-    const int32_t sp = pl.splits, ncg = pl.n_cg;
+    const int32_t sp = pl.splits;
     dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
 #define LB_SKD(AMV, GV, CV, MRV)                                                                                  \
   hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, skinny::EPI_STORE, GV, CV, MRV>), grid,                  \
-                     dim3(skinny::kThreads), pl.lds, st, av, reinterpret_cast<const uint32_t*>(b), s, c, workspace, \
-                     partial, (int)m, (int)n, (int)k, sp, ncg, nullptr, nullptr, nullptr)
+                     dim3(skinny::kThreads), pl.lds, st, av, reinterpret_cast<const uint32_t*>(b), s, (int)m, (int)n, \
+                     (int)k, sp, partial, workspace, c, nullptr, nullptr, nullptr)
 #define LB_SKDG(AMV, CV, MRV)                               \
   do {                                                      \
     if (grouped) LB_SKD(AMV, true, CV, MRV);                \
@@ -465,7 +465,7 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
     dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
 #define LB_SK(AMV, EPV, GV, CV) \
   hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, EPV, GV, CV>), grid, dim3(skinny::kThreads), pl.lds, st, \
-                     p.a, p.b, p.s, p.c, p.counters, p.partial, p.m, p.n, p.k, p.splits, p.n_cg, p.tile_keys,     \
+                     p.a, p.b, p.s, p.m, p.n, p.k, p.splits, p.partial, p.counters, p.c, p.tile_keys,             \
                      p.argmax_state, p.argmax_out)
 #define LB_SKC(AMV, EPV, GV)                              \
   do {                                                    \

@@ -319,12 +319,11 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   extern __shared__ __attribute__((aligned(16))) unsigned char smem[];
   __shared__ int s_prev;
   __shared__ uint64_t s_keys[kWaves][kMaxM];
-  // Every kernel argument the prologue needs, fetched in one round trip
-  // (left to itself the compiler loads the split fields, divides, and only
-  // then loads the pointers: two dependent kernarg fetches before the first
-  // weight load).
-  asm volatile("" ::"s"(p.a), "s"(p.b), "s"(p.s), "s"(p.counters), "s"(p.partial), "s"(p.m), "s"(p.n), "s"(p.k),
-               "s"(p.splits), "s"(p.kp_total));
+  // Every kernel argument the prologue needs, named before any other work
+  // (those of marlin_skinny_kernel are preloaded; through a struct, as in
+  // the one-launch MLP, they are fetched in one round trip instead of two
+  // dependent ones: the split fields, a division, then the pointers).
+  asm volatile("" ::"s"(p.a), "s"(p.b), "s"(p.s), "s"(p.m), "s"(p.n), "s"(p.k), "s"(p.splits), "s"(p.kp_total));
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
@@ -794,19 +793,22 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   return true;
 }
 
-// The arguments the prologue needs come first, as separate scalars: gfx950
-// preloads the leading kernel arguments into SGPRs at wave launch (the build
-// asks for 16 dwords), so the first weight loads do not wait for a kernarg
-// fetch.  A struct argument is not preloaded.
+// The arguments come first that the prologue and the split hand-off need, as
+// separate scalars: gfx950 preloads the leading kernel arguments into SGPRs
+// at wave launch (14 dwords here: the build asks for 16, the kernarg pointer
+// takes two), so neither the first weight loads nor the partial stores wait
+// for a kernarg fetch.  a, b, s, the four sizes and the two hand-off pointers
+// fill all 14; the output and argmax pointers follow.  The column-tile count
+// is n / (64 CPW).  A struct argument is not preloaded.
 template <int AM, int EPI, bool GROUPED, int CPW, int MR = 1>
 __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(const uint16_t* a, const uint32_t* b,
-                                                                 const uint16_t* s, uint16_t* c, int32_t* counters,
-                                                                 float* partial, int m, int n, int k, int splits,
-                                                                 int n_cg, uint64_t* tile_keys, int64_t* argmax_state,
+                                                                 const uint16_t* s, int m, int n, int k, int splits,
+                                                                 float* partial, int32_t* counters, uint16_t* c,
+                                                                 uint64_t* tile_keys, int64_t* argmax_state,
                                                                  int64_t* argmax_out) {
   Params p{};
   p.a = a; p.b = b; p.s = s; p.c = c; p.counters = counters; p.partial = partial;
-  p.m = m; p.n = n; p.k = k; p.splits = splits; p.kp_total = k >> 5; p.n_cg = n_cg;
+  p.m = m; p.n = n; p.k = k; p.splits = splits; p.kp_total = k >> 5; p.n_cg = n / (64 * CPW);
   p.tile_keys = tile_keys; p.argmax_state = argmax_state; p.argmax_out = argmax_out;
   skinny_tile<AM, EPI, GROUPED, CPW, MR>(p, blockIdx.x, blockIdx.y);
 }
