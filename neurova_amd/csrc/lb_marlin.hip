@@ -891,7 +891,8 @@ extern "C" int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qwe
     const size_t lds = std::max(u2.lds, (size_t)batch * skinny::kCols * 4);
     dim3 grid((unsigned)u2.n_cg, (unsigned)u2.splits, 1);
 #define LB_ACT(AMV, GV, CV, MRV) \
-  hipLaunchKernelGGL((mlp::mlp_gate_up_act_kernel<AMV, GV, CV, MRV>), grid, dim3(skinny::kThreads), lds, st, u)
+  hipLaunchKernelGGL((mlp::mlp_gate_up_act_kernel<AMV, GV, CV, MRV>), grid, dim3(skinny::kThreads), lds, st, u.a, u.b, \
+                     u.s, u.m, u.n, u.k, u.splits, u.partial, u.counters, u.act_out)
 #define LB_ACTG(AMV, CV, MRV)                   \
   do {                                          \
     if (g1) LB_ACT(AMV, true, CV, MRV);         \
