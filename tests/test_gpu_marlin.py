@@ -175,11 +175,13 @@ def test_gemm_vs_oracle(dev, m):
         assert exact > 0.95
 
 
-@pytest.mark.parametrize("m,k,n,group", [(40, 8192, 1024, 128), (64, 17408, 1280, -1), (100, 4096, 2048, 128)])
+@pytest.mark.parametrize("m,k,n,group", [(40, 8192, 1024, 128), (64, 17408, 1280, -1), (100, 4096, 2048, 128),
+                                         (128, 5120, 4352, 128), (256, 8192, 2048, -1)])
 def test_gemm_split_collect_vs_oracle(dev, m, k, n, group):
-    """Prefill tiles below 128 rows split many ways over K: the last arrival
-    of a tile reads every split (its own included) in batches and sums them
-    in split order; both scale modes, repeated launches bit-identical."""
+    """Prefill tiles split over K (3 to 8 ways): below 128 rows the last
+    arrival of a tile reads every split (its own included) in batches, on
+    128-row tiles one split per round trip with its own from registers; both
+    sum in split order.  Both scale modes, repeated launches bit-identical."""
     print_case("gemm-collect", m, k, n, group)
     codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=2100 + m)
     got = _run_gemm(dev, x, qw, sp, group)
