@@ -11,7 +11,7 @@ and ``--steps`` replays of it are timed with HIP events on the launch stream
 (``--warmup`` untimed replays first), so the timed region is
 ``steps x sets`` back-to-back kernels.
 
-Extra fields report the other BASELINE configs: M=4/16 decode, the M=2048
+Extra fields report the other BASELINE.json configs: M=4/16 decode, the M=2048
 prefill GEMM in TFLOP/s (both shapes), the rowwise fallback sweep, the
 64-layer decode-step projection sweep, and the streaming-read ceiling of the
 device (a kernel that only reads the same bytes).  ``cpu_baseline`` times a
@@ -157,7 +157,7 @@ def calls_per_step_for(n_sets, calls):
 
 
 class DecodeStep:
-    """BASELINE configs[4]: the projections of a 64-layer 27B-class decode step.
+    """BASELINE.json configs[4]: the projections of a 64-layer 27B-class decode step.
 
     Per layer: QKV 5120->7168, O 5120->5120, gate/up 5120->2x17408 (one fused
     Marlin tensor whose output is the [gate | up] `mixed` row) and down
@@ -352,7 +352,7 @@ def cpu_baseline(m, k, n, budget_s=12.0):
 
 
 def cpu_rowwise_cfg1(budget_s=6.0):
-    """BASELINE configs[0]: the reference's CPU rowwise path (LowBitTensor.gemv's
+    """BASELINE.json configs[0]: the reference's CPU rowwise path (LowBitTensor.gemv's
     CPU branch, loader.py:170-171 over dequantize_lowbit_rows, :427-465) in
     vectorised torch-CPU on the physical cores, x [4096], W [4096, 4096] b4
     g128, seed 0: (a) dequant + fp16 matmul per call, (b) the matmul alone on
@@ -409,7 +409,7 @@ def pmc_probe(torch, lc, dev, calls=24):
 
 
 def gemm_probe(torch, lc, dev, calls=6):
-    """Eager prefill GEMM calls of both BASELINE configs[2] shapes, for the
+    """Eager prefill GEMM calls of both BASELINE.json configs[2] shapes, for the
     MFMA / clock counter runs (a few warm-up calls first)."""
     for (k, n) in ((5120, 17408), (17408, 5120)):
         prob = MarlinProblem(torch, dev, 2048, k, n, 1, seed=11)

@@ -220,7 +220,7 @@ void lb_marlin_mlp_fused_set_spin_limit(int32_t polls);
  * lb_marlin_noalloc_scratch_limit() bytes (32 MiB) that each GPU holds until
  * the process ends; problems whose plan needs more return
  * LB_ERR_NOALLOC_LIMIT before anything is launched (every decode shape up to
- * M = 64 of the BASELINE projections fits; M = 2048 prefill does not).  All
+ * M = 64 of the BASELINE.json projections fits; M = 2048 prefill does not).  All
  * calls on one GPU share that array: calls that overlap (other streams) race
  * and must be serialised by the caller.  Same arguments, workspace contract
  * and results as lb_marlin_gemm. */

@@ -288,7 +288,7 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // `argmax`: the fused-argmax variant; `allow_direct`: false plans only the
 // staged decode tiles (the one-launch MLP's phases).
 //
-// Which decode form (measured on the BASELINE decode shapes): the direct
+// Which decode form (measured on the decode shapes of BASELINE.json): the direct
 // form where the tiles are narrow (the waves of a workgroup then share
 // little A, and staging the whole slice before the loop holds them up), or
 // where LDS forces the staged form to more splits than one wave of resident

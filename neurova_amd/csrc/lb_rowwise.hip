@@ -549,7 +549,7 @@ int launch_lds_bits(const Params& p, hipStream_t st) {
   const bool pairs = ((p.cols >> 5) & 1) == 0;
   // Lane steps prefetched before the staging: enough to cover the row (one
   // flood of requests, no second round trip for the row's tail), up to
-  // kLdsPreMax, so that the workgroups of a BASELINE rowwise launch stay
+  // kLdsPreMax, so that the workgroups of a BASELINE.json rowwise launch stay
   // resident at once.
   const int upl = (B == 2 && pairs) ? 2 : 1;
   const int64_t steps = ((p.cols >> 5) + upl * kWave - 1) / (upl * kWave);
@@ -583,7 +583,7 @@ int launch_lds_bits(const Params& p, hipStream_t st) {
 
 // Workgroup shape of the one-row kernel.  A workgroup stages the whole
 // activation row in LDS, so fewer, wider workgroups stage it fewer times;
-// the shapes below give the BASELINE configs one workgroup per CU where that
+// the shapes below give the BASELINE.json configs one workgroup per CU where that
 // measured faster (one process, graph replay, against 8 waves of one row):
 //   8 bits, 5120 x 17408:  10 waves of 2 rows (256 workgroups) 18.5 us against 21.2 us;
 //   4 bits, 4096 x 4096:   16 waves of 1 row  (256 workgroups)  3.66 us against 3.95 us.

@@ -193,7 +193,7 @@ def test_gemm_split_collect_vs_oracle(dev, m, k, n, group):
 
 @pytest.mark.parametrize("m", [1, 4, 16, 32])
 def test_decode_shape_cfg2(dev, m):
-    """BASELINE configs[1]: M in {1,4,16}, K=5120, N=17408, g=128 (and configs[4]'s M=32)."""
+    """BASELINE.json configs[1]: M in {1,4,16}, K=5120, N=17408, g=128 (and configs[4]'s M=32)."""
     k, n = 5120, 17408
     print_case("cfg2", m, k, n)
     _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=7)
@@ -290,7 +290,7 @@ def test_small_m_gemm_many_splits_vs_oracle(dev, m):
 
 @pytest.mark.parametrize("k,n", [(5120, 17408), (17408, 5120)])
 def test_prefill_shape_cfg3(dev, k, n):
-    """BASELINE configs[2]: M=2048; a bounded row sample is checked against the oracle."""
+    """BASELINE.json configs[2]: M=2048; a bounded row sample is checked against the oracle."""
     m = 2048
     print_case("cfg3", m, k, n)
     _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=9)

@@ -3,7 +3,7 @@
 Follows the reference's tests langburst/tests/test_lowbit_gemv_cuda.py:14-73
 (GEMV vs CPU dequant, pair == two singles, GEMM == repeated GEMV) and
 langburst/tests/test_v05_cuda_kernels.py:19-32 (row dequant known answers),
-at the reference's odd sizes (K = 513, 257, 259) and BASELINE's full sizes.
+at the reference's odd sizes (K = 513, 257, 259) and the full sizes of BASELINE.json.
 """
 from __future__ import annotations
 
@@ -160,7 +160,7 @@ def test_gemm_equals_repeated_gemv(dev, bits, cols, batch):
 
 
 def test_cfg1_full_size(dev):
-    """BASELINE configs[0]: N=K=4096, b4, g128, M=1."""
+    """BASELINE.json configs[0]: N=K=4096, b4, g128, M=1."""
     _, packed, scales, x = O.make_rowwise_inputs(4096, 4096, 4, 128, seed=0)
     got = _gemv(dev, packed, scales, x[0], 4096, 128, 4)
     exact = assert_close_f16(got, O.rowwise_gemv(packed, scales, x[0], 4096, 128, 4), what="cfg1")
@@ -182,7 +182,7 @@ def test_wide_workgroup_shapes_vs_oracle(dev, bits, rows, cols):
 @pytest.mark.parametrize("bits", [2, 3, 8])
 @pytest.mark.parametrize("group", [64, 128])
 def test_cfg4_full_size(dev, bits, group):
-    """BASELINE configs[3]: M=1, K=17408, N=5120, b in {2,3,8}, g in {64,128}."""
+    """BASELINE.json configs[3]: M=1, K=17408, N=5120, b in {2,3,8}, g in {64,128}."""
     print_case("cfg4", bits, group)
     _, packed, scales, x = O.make_rowwise_inputs(5120, 17408, bits, group, seed=bits + group)
     got = _gemv(dev, packed, scales, x[0], 17408, group, bits)

@@ -3,7 +3,7 @@
 Each entry point plans its launch on the host: the decode form (A staged whole,
 A fragments loaded per step, A through an LDS ring) or the prefill GEMM, the
 tile width, the k splits, the LDS, scratch and workspace it needs.  These tests
-sweep the BASELINE shapes and edge shapes and check the invariants the kernels
+sweep the BASELINE.json shapes and edge shapes and check the invariants the kernels
 rely on (every wave gets a scale group, LDS within a workgroup's 64 KB, the
 workspace within the reference's N/128*16 entries, the split arithmetic within
 32 bits) and the rules the measurements chose (``make_plan`` in
@@ -36,7 +36,7 @@ def _plan(m, n, k, g=128, variant=0, ws=None):
 def test_plan_invariants(L, variant):
     for m, n, k in itertools.product(MS, NS, KS):
         if variant == 1 and m > 64 and n > 17408:
-            continue  # the SiLU-gated op at prefill sizes is covered by the BASELINE shapes below
+            continue  # the SiLU-gated op at prefill sizes is covered by the BASELINE.json shapes below
         p = _plan(m, n, k, 128, variant)
         what = f"m={m} n={n} k={k} variant={variant}: {p}"
         assert p["workgroups"] >= 1, what
