@@ -191,6 +191,29 @@ def test_gemm_split_collect_vs_oracle(dev, m, k, n, group):
     assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
 
 
+@pytest.mark.parametrize("m,k,n,group", [(256, 5120, 17408, 128), (384, 17408, 5120, 128), (200, 16384, 4096, -1),
+                                         (2048, 17408, 5120, 128)])
+def test_gemm_all_tiles_split_vs_oracle(dev, m, k, n, group):
+    """Fewer 128-row tiles than resident workgroups: every tile is split over
+    K (3 or 5 ways, up to 960 workgroups), a ragged last row block (M = 200),
+    both scale modes.  Sampled rows cover every tile; repeated launches are
+    bit-identical and the workspace is left zero."""
+    from neurova_amd import capi
+
+    plan = capi.marlin_describe_plan(m, n, k, group)
+    assert plan["form"] == "prefill" and plan["row_blocks_or_full_tiles"] == 0 and plan["splits"] > 1, plan
+    print_case("gemm-all-split", m, k, n, group, plan["splits"])
+    codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=2500 + m)
+    got = _run_gemm(dev, x, qw, sp, group)
+    rows = np.unique(np.concatenate([np.arange(0, m, 37), [1, 127, 128, 129, m - 2, m - 1]]))
+    rows = rows[rows < m]
+    exact = assert_close_f16(got[rows], O.marlin_gemm(x, qw, sp, group, rows=rows),
+                             what=f"gemm-all-split m={m} k={k} n={n} g={group}")
+    assert exact > 0.9
+    again = _run_gemm(dev, x, qw, sp, group)
+    assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
+
+
 @pytest.mark.parametrize("m", [1, 4, 16, 32])
 def test_decode_shape_cfg2(dev, m):
     """M in {1,4,16}, K=5120, N=17408, g=128 (and configs[4]'s M=32)."""
