@@ -166,8 +166,9 @@ class DecodeStep:
     packed weights, all resident (about 10.9 GB).  fused_mlp: gate/up, SiLU
     and down as one lb_marlin_mlp_fused call asking for one launch (mode 1: one
     launch where both projections plan the same tiles as the two calls, here
-    M <= 4; the two calls otherwise), whose output is bit-identical to the two
-    calls.  A call is one op of the C ABI; the SiLU-gated down projection at
+    M <= 4; at M = 16 and 32 two launches, gate/up tiles storing
+    fp16(silu(g) * u) and then down over those activations), whose output is
+    bit-identical to the two calls.  A call is one op of the C ABI; the SiLU-gated down projection at
     M >= 5 is two kernel launches (the gated activations first)."""
 
     HIDDEN, INTER, QKV, O_IN = 5120, 17408, 7168, 5120
@@ -645,9 +646,9 @@ def main():
         for mm in (1, 4, 16, 32):
             extra[f"decode_step_64_layers_m{mm}"] = r = decode_step_sweep(torch, lc, dev, mm)
             log(f"[bench] 64-layer decode step M={mm}: {r['us_per_step']:.1f} us, {r['GB/s']:.1f} GB/s")
-        for mm in (4, 16):
+        for mm in (4, 16, 32):
             extra[f"decode_step_64_layers_m{mm}_fused_mlp"] = r = decode_step_sweep(torch, lc, dev, mm, fused_mlp=True)
-            log(f"[bench] 64-layer decode step M={mm}, one-launch MLP: {r['us_per_step']:.1f} us, "
+            log(f"[bench] 64-layer decode step M={mm}, lb_marlin_mlp_fused mode 1: {r['us_per_step']:.1f} us, "
                 f"{r['calls_per_step']} calls")
         result["extra"] = extra
 
