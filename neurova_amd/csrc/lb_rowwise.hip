@@ -219,6 +219,23 @@ __host__ __device__ constexpr int pair_hi(int bits, int q) {
 __host__ __device__ constexpr int n_classes(int bits) { return bits == 2 ? 5 : bits == 3 ? 8 : bits == 4 ? 2 : 1; }
 __host__ __device__ constexpr int class_of_off(int bits, int off) { return bits == 2 ? off / 2 : bits == 4 ? off / 4 : off; }
 __host__ __device__ constexpr int off_of_class(int bits, int c) { return bits == 2 ? 2 * c : bits == 4 ? 4 * c : c; }
+// The first pair q (in 0..15) of offset class c.
+__host__ __device__ constexpr int pair_off(int bits, int q);
+__host__ __device__ constexpr int first_pair_of_class(int bits, int c) {
+  int q = 0;
+  while (q < 15 && class_of_off(bits, pair_off(bits, q)) != c) ++q;
+  return q;
+}
+
+// x.lo * y.lo + x.hi * y.hi in fp32 (fp16 pairs), starting from zero: the
+// three-operand v_dot2_f32_f16 with an inline 0, where the compiler would
+// otherwise pick the accumulating two-operand form and a move of 0.
+__device__ __forceinline__ float dot2_from_zero(uint32_t x, uint32_t y) {
+  float r;
+  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(x), "v"(y));
+  return r;
+}
+
 __host__ __device__ constexpr int pair_off(int bits, int q) {
   return bits == 2 ? ((q & 7) < 5 ? 2 * (q & 7) : 2 * (q & 7) - 6)
        : bits == 3 ? (q == 0 ? 0 : q == 1 ? 3 : q == 2 ? 6 : q == 3 ? 3 : q == 4 ? 6 : q == 5 ? 2 : q == 6 ? 5
@@ -335,8 +352,9 @@ __global__ __launch_bounds__(W * kWave) void rowwise_lds_kernel(const uint8_t* q
         const uint32_t* src = qrow[a][r] + (uint32_t)u0 * BITS;
 #pragma unroll
         for (int d = 0; d < kStepWords; ++d) w[a][r][d] = __builtin_nontemporal_load(src + d);
+        // (UPL = 2: the pair shares one group's scale, sc[0])
 #pragma unroll
-        for (int j = 0; j < UPL; ++j) sc[j][a][r] = h2f(srow[a][r][(uint32_t)(u0 + j) >> unit_shift]);
+        for (int j = 0; j < (UPL == 2 ? 1 : UPL); ++j) sc[j][a][r] = h2f(srow[a][r][(uint32_t)(u0 + j) >> unit_shift]);
       }
   };
   // ---- the activation row's loads first (at most kStageUnits units per
@@ -397,12 +415,59 @@ __global__ __launch_bounds__(W * kWave) void rowwise_lds_kernel(const uint8_t* q
   for (int a = 0; a < NW; ++a)
 #pragma unroll
     for (int r = 0; r < R; ++r) acc[a][r] = 0.f;
-  // With UPL = 2 (2 bits, even unit count) a lane takes two adjacent units
-  // per step, so each code load is 16 contiguous bytes: wider loads per
-  // instruction move the weight stream faster.  A lane adds its units in
+  // With UPL = 2 (2 bits, even unit count, group >= 64 codes) a lane takes
+  // two adjacent units of one scale group per step, so each code load is 16
+  // contiguous bytes: wider loads per instruction move the weight stream
+  // faster.  The pair is summed as one unit of 64 codes: one set of offset
+  // class sums, one z * sum(x) correction, one scale multiply (VALU is what
+  // bounds 2 bits: 83 instead of 94 per step).  A lane adds its steps in
   // increasing order.
   auto step = [&](int u0, const uint32_t (&w)[NW][R][kStepWords], const float (&sc)[UPL][NW][R])
       __attribute__((always_inline)) {
+    if constexpr (UPL == 2) {
+      constexpr int NC = n_classes(BITS);
+      float tc[NW][R][NC];  // each set by its class's first pair of the first unit
+      float cu = 0.f;
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const int u = u0 + j;
+        uint32_t xq[16];
+#pragma unroll
+        for (int v = 0; v < 4; ++v) {
+          const u32x4 t4 = xt[v * units + u];
+          xq[4 * v] = t4[0];
+          xq[4 * v + 1] = t4[1];
+          xq[4 * v + 2] = t4[2];
+          xq[4 * v + 3] = t4[3];
+        }
+        cu += corr[u];
+#pragma unroll
+        for (int a = 0; a < NW; ++a)
+#pragma unroll
+          for (int r = 0; r < R; ++r) {
+            uint32_t b[16];
+            decode_unit<BITS>(&w[a][r][j * BITS], b);
+#pragma unroll
+            for (int q = 0; q < 16; ++q) {
+              const int c = class_of_off(BITS, pair_off(BITS, q));
+              if (j == 0 && q == first_pair_of_class(BITS, c))
+                tc[a][r][c] = dot2_from_zero(b[q], xq[q]);
+              else
+                tc[a][r][c] = __builtin_amdgcn_fdot2(as_h2(b[q]), as_h2(xq[q]), tc[a][r][c], false);
+            }
+          }
+      }
+#pragma unroll
+      for (int a = 0; a < NW; ++a)
+#pragma unroll
+        for (int r = 0; r < R; ++r) {
+          float t = -cu;
+#pragma unroll
+          for (int c = 0; c < NC; ++c) t = __builtin_fmaf(tc[a][r][c], (float)(1 << (24 - off_of_class(BITS, c))), t);
+          acc[a][r] = __builtin_fmaf(t, sc[0][a][r], acc[a][r]);
+        }
+      return;
+    }
 #pragma unroll
     for (int j = 0; j < UPL; ++j) {
       const int u = u0 + j;
@@ -544,9 +609,11 @@ int launch_lds_bits(const Params& p, hipStream_t st) {
   dim3 grid((unsigned)((p.rows + rows_per_wg - 1) / rows_per_wg));
   const size_t lds = (size_t)(p.cols >> 5) * kLdsUnitBytes;
   // 2 bits: two units per lane step (16-byte code loads) where every lane's
-  // pair lies inside the row.  Measured at K = 17408: 2 bits 4 % faster; 3 bits
-  // mixed (g64 faster, g128 slower); 4 bits 15 % slower, so 3-8 bits keep one.
-  const bool pairs = ((p.cols >> 5) & 1) == 0;
+  // pair lies inside the row and inside one scale group (group >= 64 codes:
+  // the kernel then sums the pair as one).  Measured at K = 17408: 2 bits 4 %
+  // faster; 3 bits mixed (g64 faster, g128 slower); 4 bits 15 % slower, so
+  // 3-8 bits keep one.
+  const bool pairs = ((p.cols >> 5) & 1) == 0 && p.unit_shift > 0;
   // Lane steps prefetched before the staging: enough to cover the row (one
   // flood of requests, no second round trip for the row's tail), up to
   // kLdsPreMax, so that the workgroups of a BASELINE.json rowwise launch stay
