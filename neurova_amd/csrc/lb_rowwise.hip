@@ -219,23 +219,6 @@ __host__ __device__ constexpr int pair_hi(int bits, int q) {
 __host__ __device__ constexpr int n_classes(int bits) { return bits == 2 ? 5 : bits == 3 ? 8 : bits == 4 ? 2 : 1; }
 __host__ __device__ constexpr int class_of_off(int bits, int off) { return bits == 2 ? off / 2 : bits == 4 ? off / 4 : off; }
 __host__ __device__ constexpr int off_of_class(int bits, int c) { return bits == 2 ? 2 * c : bits == 4 ? 4 * c : c; }
-// The first pair q (in 0..15) of offset class c.
-__host__ __device__ constexpr int pair_off(int bits, int q);
-__host__ __device__ constexpr int first_pair_of_class(int bits, int c) {
-  int q = 0;
-  while (q < 15 && class_of_off(bits, pair_off(bits, q)) != c) ++q;
-  return q;
-}
-
-// x.lo * y.lo + x.hi * y.hi in fp32 (fp16 pairs), starting from zero: the
-// three-operand v_dot2_f32_f16 with an inline 0, where the compiler would
-// otherwise pick the accumulating two-operand form and a move of 0.
-__device__ __forceinline__ float dot2_from_zero(uint32_t x, uint32_t y) {
-  float r;
-  asm("v_dot2_f32_f16 %0, %1, %2, 0" : "=v"(r) : "v"(x), "v"(y));
-  return r;
-}
-
 __host__ __device__ constexpr int pair_off(int bits, int q) {
   return bits == 2 ? ((q & 7) < 5 ? 2 * (q & 7) : 2 * (q & 7) - 6)
        : bits == 3 ? (q == 0 ? 0 : q == 1 ? 3 : q == 2 ? 6 : q == 3 ? 3 : q == 4 ? 6 : q == 5 ? 2 : q == 6 ? 5
@@ -419,14 +402,19 @@ __global__ __launch_bounds__(W * kWave) void rowwise_lds_kernel(const uint8_t* q
   // two adjacent units of one scale group per step, so each code load is 16
   // contiguous bytes: wider loads per instruction move the weight stream
   // faster.  The pair is summed as one unit of 64 codes: one set of offset
-  // class sums, one z * sum(x) correction, one scale multiply (VALU is what
-  // bounds 2 bits: 83 instead of 94 per step).  A lane adds its steps in
-  // increasing order.
+  // class sums, one z * sum(x) correction, one scale multiply (85 instead
+  // of 94 VALU per step).  A lane adds its steps in increasing order.
   auto step = [&](int u0, const uint32_t (&w)[NW][R][kStepWords], const float (&sc)[UPL][NW][R])
       __attribute__((always_inline)) {
     if constexpr (UPL == 2) {
       constexpr int NC = n_classes(BITS);
-      float tc[NW][R][NC];  // each set by its class's first pair of the first unit
+      float tc[NW][R][NC];
+#pragma unroll
+      for (int a = 0; a < NW; ++a)
+#pragma unroll
+        for (int r = 0; r < R; ++r)
+#pragma unroll
+          for (int c = 0; c < NC; ++c) tc[a][r][c] = 0.f;
       float cu = 0.f;
 #pragma unroll
       for (int j = 0; j < 2; ++j) {
@@ -450,10 +438,7 @@ __global__ __launch_bounds__(W * kWave) void rowwise_lds_kernel(const uint8_t* q
 #pragma unroll
             for (int q = 0; q < 16; ++q) {
               const int c = class_of_off(BITS, pair_off(BITS, q));
-              if (j == 0 && q == first_pair_of_class(BITS, c))
-                tc[a][r][c] = dot2_from_zero(b[q], xq[q]);
-              else
-                tc[a][r][c] = __builtin_amdgcn_fdot2(as_h2(b[q]), as_h2(xq[q]), tc[a][r][c], false);
+              tc[a][r][c] = __builtin_amdgcn_fdot2(as_h2(b[q]), as_h2(xq[q]), tc[a][r][c], false);
             }
           }
       }
