@@ -168,8 +168,9 @@ class DecodeStep:
     launch where both projections plan the same tiles as the two calls, here
     M <= 4; at M = 16 and 32 two launches, gate/up tiles storing
     fp16(silu(g) * u) and then down over those activations), whose output is
-    bit-identical to the two calls.  A call is one op of the C ABI; the SiLU-gated down projection at
-    M >= 5 is two kernel launches (the gated activations first)."""
+    bit-identical to the two calls.  A call is one op of the C ABI; the
+    SiLU-gated down projection at M >= 5 is two kernel launches (the gated
+    activations first)."""
 
     HIDDEN, INTER, QKV, O_IN = 5120, 17408, 7168, 5120
 
