@@ -165,7 +165,8 @@ struct Plan {
   int n_mb = 1;
   int n_cg = 0;      // column tiles (decode: 64 * cpw columns; GEMM: 256)
   int cpw = 4;       // decode: chunks (64 columns) per workgroup
-  int splits = 1;    // decode: K splits of every column tile
+  int splits = 1;    // decode: K splits of every column tile (mixed plans: of the tiles past `whole`)
+  int whole = 0;     // decode, mixed plan: the first `whole` tiles run over the whole K, unsplit
   int full_tiles = 0;   // GEMM: tiles computed whole
   int tail_tiles = 0;   // GEMM: tiles split over K ...
   int tail_splits = 1;  // ... this many ways
@@ -298,10 +299,42 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // pay below 5 rows.  M = 17..32: the direct form on 64-column tiles, the
 // ring on 4-chunk tiles; 2-chunk tiles go to the prefill kernel.
 inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am, bool argmax = false,
-                      bool allow_direct = true) {
+                      bool allow_direct = true, bool allow_mixed = true) {
   Plan pl;
   pl.n_cg = (int)(n / 256);
   const int groups = (int)(k / 128);
+  // One row of A, grouped scales, where the 64-column chunks number between one and two per CU:
+  // one single-chunk tile per CU over the whole K (its four waves' k shares
+  // summed in LDS, no split-K hand-off), and the leftover chunks split over K
+  // among at most one more workgroup per CU.  One whole-K single-chunk tile
+  // per CU measured 11.6 against 13.0 us at K = 5120, N = 16384, and the
+  // headline shape (N = 17408) 12.45 against 13.38 us.  With one scale per
+  // column it measured slower (13.7 against 12.6 us), so that keeps the split
+  // 4-chunk tiles (`allow_mixed` false).
+  if (m == 1 && allow_direct && allow_mixed && !argmax && am == gemm::A_PLAIN) {
+    const int64_t chunks = n / 64, cus = device_cus();
+    const int ksub = skinny::kWaves;  // 1-chunk tiles: the four waves share the k range
+    // (measured at K <= 5120 and up to CUs / 8 leftover chunks; a longer K or
+    // more leftover work per CU keeps the split tiles)
+    if (chunks >= cus && (chunks - cus) * 8 <= cus && groups >= ksub && k <= 5120) {
+      const int64_t left = chunks - cus;
+      const int s = left > 0 ? (int)std::min<int64_t>(std::min<int64_t>(cus / left, groups / ksub), 256) : 1;
+      if (left == 0 || (s >= 2 && workspace_len >= 1 + chunks)) {
+        pl.skinny = true;
+        pl.direct = false;
+        pl.mr = 1;
+        pl.cpw = 1;
+        pl.n_cg = (int)chunks;
+        pl.whole = (int)cus;
+        pl.splits = s;
+        pl.x_bytes = (size_t)groups * 128 * (size_t)m * 2;
+        pl.lds = std::max(pl.x_bytes + 16, (size_t)m * skinny::kCols * 4);
+        pl.partial_bytes = left > 0 ? align_up((size_t)s * (size_t)m * (size_t)n * 4) : 0;
+        pl.keys_bytes = align_up((size_t)m * (size_t)pl.n_cg * 8);
+        return pl;
+      }
+    }
+  }
   const Tiling ts = m <= skinny::kMaxM ? staged_tiling(m, n, k, workspace_len) : Tiling{};
   const Tiling td = (allow_direct && !argmax && m <= 16 * skinny::kMaxMR) ? direct_tiling(m, n, k, workspace_len)
                                                                          : Tiling{};
@@ -408,7 +441,8 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   const int64_t a_bytes = m * k * 2 * (var == V_SILU ? 2 : 1);
   if (m > skinny::kMaxM && (a_bytes >= (1LL << 31) || k * n / 2 >= (1LL << 31))) return LB_ERR_PROB_SHAPE;
   const bool gated = var == V_SILU || var == V_SILU_DONE;
-  const Plan pl = make_plan(m, n, k, workspace_len, gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, var == V_ARGMAX);
+  const Plan pl = make_plan(m, n, k, workspace_len, gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, var == V_ARGMAX,
+                            true, grouped != 0);
   if (var == V_SILU_DONE && !pl.skinny) return LB_ERR_ARG;  // decode batches only
   if (workspace_len < counters_needed(pl, var == V_ARGMAX)) return LB_ERR_WORKSPACE;
   const size_t need = pl.partial_bytes + (var == V_ARGMAX ? pl.keys_bytes : 0) + (var == V_SILU ? pl.act_bytes : 0);
@@ -462,11 +496,12 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
     p.argmax_state = argmax_state; p.argmax_out = argmax_out;
     p.m = (int)m; p.n = (int)n; p.k = (int)k; p.splits = pl.splits;
     p.kp_total = (int)(k / 32); p.n_cg = pl.n_cg;
-    dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
+    const dim3 grid = pl.whole > 0 ? dim3((unsigned)(pl.whole + (int64_t)(pl.n_cg - pl.whole) * pl.splits), 1, 1)
+                                   : dim3((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
 #define LB_SK(AMV, EPV, GV, CV) \
   hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, EPV, GV, CV>), grid, dim3(skinny::kThreads), pl.lds, st, \
-                     p.a, p.b, p.s, p.m, p.n, p.k, p.splits, p.partial, p.counters, p.c, p.tile_keys,             \
-                     p.argmax_state, p.argmax_out)
+                     p.a, p.b, p.s, p.m, p.n, p.k, (pl.whole << 16) | p.splits, p.partial, p.counters, p.c,        \
+                     p.tile_keys, p.argmax_state, p.argmax_out)
 #define LB_SKC(AMV, EPV, GV)                              \
   do {                                                    \
     if (pl.cpw == 4) LB_SK(AMV, EPV, GV, 4);              \
@@ -545,10 +580,13 @@ extern "C" size_t lb_marlin_scratch_bytes(int64_t prob_m, int64_t prob_n, int64_
   if (prob_m <= 0 || prob_n <= 0 || prob_k <= 0 || prob_n % 256 || prob_k % 128) return 0;
   // Plan with an unconstrained workspace: the largest scratch any plan uses.
   // Largest over the variants (the SiLU-gated one may use other tiles).
+  // (with and without the mixed plan, which only grouped scales take)
   const marlin::Plan a = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN);
+  const marlin::Plan a2 = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN, false, true, false);
   const marlin::Plan b = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_SILU_PACKED);
   const marlin::Plan c = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN, true);
-  return std::max(std::max(a.partial_bytes + a.keys_bytes, b.partial_bytes + b.keys_bytes + b.act_bytes),
+  return std::max(std::max(std::max(a.partial_bytes + a.keys_bytes, a2.partial_bytes + a2.keys_bytes),
+                           b.partial_bytes + b.keys_bytes + b.act_bytes),
                   c.partial_bytes + c.keys_bytes);
 }
 
@@ -562,13 +600,13 @@ extern "C" int lb_marlin_describe_plan(int64_t prob_m, int64_t prob_n, int64_t p
   if (prob_m == 0 || prob_n == 0 || prob_k == 0) return LB_OK;
   const bool argmax = variant == 2, gated = variant == 1;
   const marlin::Plan pl = marlin::make_plan(prob_m, prob_n, prob_k, workspace_len,
-                                            gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, argmax);
+                                            gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, argmax, true, grouped != 0);
   if (pl.skinny) {
     out[0] = !pl.direct ? 0 : pl.cpw == skinny::kWaves ? 2 : 1;
     out[1] = pl.cpw;
     out[2] = pl.splits;
     out[3] = pl.mr;
-    out[4] = (int64_t)pl.n_cg * pl.splits;
+    out[4] = pl.whole > 0 ? pl.whole + (int64_t)(pl.n_cg - pl.whole) * pl.splits : (int64_t)pl.n_cg * pl.splits;
     out[5] = (int64_t)pl.lds;
   } else {
     out[0] = 3;

@@ -806,11 +806,31 @@ __global__ __launch_bounds__(kThreads) void marlin_skinny_kernel(const uint16_t*
                                                                  float* partial, int32_t* counters, uint16_t* c,
                                                                  uint64_t* tile_keys, int64_t* argmax_state,
                                                                  int64_t* argmax_out) {
+  // `splits` carries the mixed plan's whole-tile count in its high 16 bits, so
+  // that the mapping below reads only preloaded arguments
+  const int whole = (int)((uint32_t)splits >> 16);
+  splits &= 0xffff;
   Params p{};
   p.a = a; p.b = b; p.s = s; p.c = c; p.counters = counters; p.partial = partial;
   p.m = m; p.n = n; p.k = k; p.splits = splits; p.kp_total = k >> 5; p.n_cg = n / (64 * CPW);
   p.tile_keys = tile_keys; p.argmax_state = argmax_state; p.argmax_out = argmax_out;
-  skinny_tile<AM, EPI, GROUPED, CPW, MR>(p, blockIdx.x, blockIdx.y);
+  int cg = blockIdx.x, split = blockIdx.y;
+  if (whole > 0) {
+    // Mixed grid (one dimension): tiles 0 .. whole - 1 over the whole K (their
+    // waves' k shares summed in LDS, no split-K hand-off), the remaining tiles
+    // split `splits` ways.
+    const int bid = blockIdx.x;
+    if (bid < whole) {
+      cg = bid;
+      split = 0;
+      p.splits = 1;
+    } else {
+      const int u = bid - whole;
+      cg = whole + u / splits;
+      split = u - (u / splits) * splits;
+    }
+  }
+  skinny_tile<AM, EPI, GROUPED, CPW, MR>(p, cg, split);
 }
 
 // SiLU-gated activations for the A_DIRECT launches: act[m][k] =

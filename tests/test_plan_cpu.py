@@ -49,7 +49,13 @@ def test_plan_invariants(L, variant):
             continue
         cpw, s, mr = p["chunks_or_row_blocks"], p["splits"], p["row_blocks_or_full_tiles"]
         assert cpw in (1, 2, 4) and 1 <= s <= 256, what
-        assert p["workgroups"] == (n // (64 * cpw)) * s, what
+        chunks, cus = n // 64, p["cus"]
+        if cpw == 1 and m == 1 and p["workgroups"] != chunks * s:
+            # mixed: one whole-K single-chunk tile per CU, the leftover chunks split s ways
+            assert p["form"] == "staged" and cus < chunks and (chunks - cus) * 8 <= cus and k <= 5120, what
+            assert p["workgroups"] == cus + (chunks - cus) * s, what
+        else:
+            assert p["workgroups"] == (n // (64 * cpw)) * s, what
         assert p["lds_bytes"] <= LDS_LIMIT, what
         # every wave of a tile gets at least one scale group of its split
         assert (k // 128) // s >= 4 // cpw, what
@@ -66,9 +72,14 @@ def test_plan_invariants(L, variant):
 
 
 def test_plan_rules_at_baseline_shapes(L):
-    # headline (cfg2): staged 4-chunk tiles, 7 splits, 476 workgroups
+    # headline (cfg2): one whole-K single-chunk tile per CU (256), the 16
+    # leftover chunks split 10 ways: 416 workgroups; N = 16384: 256 whole tiles
     p = _plan(1, 17408, 5120)
-    assert (p["form"], p["chunks_or_row_blocks"], p["splits"], p["workgroups"]) == ("staged", 4, 7, 476)
+    assert (p["form"], p["chunks_or_row_blocks"], p["splits"], p["workgroups"]) == ("staged", 1, 10, 416)
+    p = _plan(1, 16384, 5120)
+    assert (p["form"], p["chunks_or_row_blocks"], p["splits"], p["workgroups"]) == ("staged", 1, 1, 256)
+    # M = 4 and K = 17408 keep the split 4-chunk tiles
+    assert (_plan(4, 17408, 5120)["chunks_or_row_blocks"], _plan(1, 17408, 17408)["chunks_or_row_blocks"]) == (4, 4)
     # narrow decode projections take 64-column direct tiles
     for m in (1, 4, 16):
         assert _plan(m, 7168, 5120)["form"] == "direct"
