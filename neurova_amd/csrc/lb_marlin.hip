@@ -298,25 +298,32 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // form first forms fp16(silu(g) * u) in a launch of its own, which does not
 // pay below 5 rows.  M = 17..32: the direct form on 64-column tiles, the
 // ring on 4-chunk tiles; 2-chunk tiles go to the prefill kernel.
+#ifndef LB_MIXED_MAX_M
+#define LB_MIXED_MAX_M 4
+#endif
+
 inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am, bool argmax = false,
                       bool allow_direct = true, bool allow_mixed = true) {
   Plan pl;
   pl.n_cg = (int)(n / 256);
   const int groups = (int)(k / 128);
-  // One row of A, grouped scales, where the 64-column chunks number between one and two per CU:
+  // Up to four rows of A, grouped scales, where the 64-column chunks number between one and two per CU:
   // one single-chunk tile per CU over the whole K (its four waves' k shares
   // summed in LDS, no split-K hand-off), and the leftover chunks split over K
   // among at most one more workgroup per CU.  One whole-K single-chunk tile
   // per CU measured 11.6 against 13.0 us at K = 5120, N = 16384, and the
   // headline shape (N = 17408) 12.45 against 13.38 us.  With one scale per
   // column it measured slower (13.7 against 12.6 us), so that keeps the split
-  // 4-chunk tiles (`allow_mixed` false).
-  if (m == 1 && allow_direct && allow_mixed && !argmax && am == gemm::A_PLAIN) {
+  // 4-chunk tiles (`allow_mixed` false).  At M = 2 and 3 (N = 17408) it measured
+  // 12.6 / 12.8 against 13.8 / 13.9 us; at M = 4 it gains where at most 4 chunks
+  // are left over (N = 16384: 12.5 against 13.6 us; K = 2048, N = 16640: 9.2
+  // against 10.1 us) and loses with 16 (N = 17408: 14.2 against 13.9 us).
+  if (m <= LB_MIXED_MAX_M && allow_direct && allow_mixed && !argmax && am == gemm::A_PLAIN) {
     const int64_t chunks = n / 64, cus = device_cus();
     const int ksub = skinny::kWaves;  // 1-chunk tiles: the four waves share the k range
     // (measured at K <= 5120 and up to CUs / 8 leftover chunks; a longer K or
     // more leftover work per CU keeps the split tiles)
-    if (chunks >= cus && (chunks - cus) * 8 <= cus && groups >= ksub && k <= 5120) {
+    if (chunks >= cus && (chunks - cus) * 8 <= cus && groups >= ksub && k <= 5120 && (m <= 3 || chunks - cus <= 4)) {
       const int64_t left = chunks - cus;
       const int s = left > 0 ? (int)std::min<int64_t>(std::min<int64_t>(cus / left, groups / ksub), 256) : 1;
       if (left == 0 || (s >= 2 && workspace_len >= 1 + chunks)) {

@@ -50,9 +50,10 @@ def test_plan_invariants(L, variant):
         cpw, s, mr = p["chunks_or_row_blocks"], p["splits"], p["row_blocks_or_full_tiles"]
         assert cpw in (1, 2, 4) and 1 <= s <= 256, what
         chunks, cus = n // 64, p["cus"]
-        if cpw == 1 and m == 1 and p["workgroups"] != chunks * s:
+        if cpw == 1 and m <= 4 and p["workgroups"] != chunks * s:
             # mixed: one whole-K single-chunk tile per CU, the leftover chunks split s ways
             assert p["form"] == "staged" and cus < chunks and (chunks - cus) * 8 <= cus and k <= 5120, what
+            assert m <= 3 or chunks - cus <= 4, what
             assert p["workgroups"] == cus + (chunks - cus) * s, what
         else:
             assert p["workgroups"] == (n // (64 * cpw)) * s, what
@@ -78,7 +79,11 @@ def test_plan_rules_at_baseline_shapes(L):
     assert (p["form"], p["chunks_or_row_blocks"], p["splits"], p["workgroups"]) == ("staged", 1, 10, 416)
     p = _plan(1, 16384, 5120)
     assert (p["form"], p["chunks_or_row_blocks"], p["splits"], p["workgroups"]) == ("staged", 1, 1, 256)
-    # M = 4 and K = 17408 keep the split 4-chunk tiles
+    # M = 2 and 3 take the mixed plan too; M = 4 only with at most 4 leftover chunks
+    for m in (2, 3):
+        assert _plan(m, 17408, 5120)["workgroups"] == 416
+    assert _plan(4, 16384, 5120)["workgroups"] == 256 and _plan(4, 16640, 2048)["workgroups"] == 256 + 4 * 4
+    # M = 4 at N = 17408 and K = 17408 keep the split 4-chunk tiles
     assert (_plan(4, 17408, 5120)["chunks_or_row_blocks"], _plan(1, 17408, 17408)["chunks_or_row_blocks"]) == (4, 4)
     # narrow decode projections take 64-column direct tiles
     for m in (1, 4, 16):
