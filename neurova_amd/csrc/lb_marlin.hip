@@ -298,6 +298,9 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // form first forms fp16(silu(g) * u) in a launch of its own, which does not
 // pay below 5 rows.  M = 17..32: the direct form on 64-column tiles, the
 // ring on 4-chunk tiles; 2-chunk tiles go to the prefill kernel.
+#ifndef LB_MIXED_MAX_PER_CU
+#define LB_MIXED_MAX_PER_CU 2
+#endif
 #ifndef LB_MIXED_MAX_M
 #define LB_MIXED_MAX_M 4
 #endif
@@ -318,13 +321,17 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
   // 12.6 / 12.8 against 13.8 / 13.9 us; at M = 4 it gains where at most 4 chunks
   // are left over (N = 16384: 12.5 against 13.6 us; K = 2048, N = 16640: 9.2
   // against 10.1 us) and loses with 16 (N = 17408: 14.2 against 13.9 us).
+  // Two whole-K tiles per CU where the chunks number two to 2 1/8 per CU
+  // (gate/up, N = 34816: 21.2 against 21.9 us; N = 33280: 19.6 against 21.4;
+  // K = 4096, N = 32768: 15.5 against 16.8 us); more per CU is not measured.
   if (m <= LB_MIXED_MAX_M && allow_direct && allow_mixed && !argmax && am == gemm::A_PLAIN) {
     const int64_t chunks = n / 64, cus = device_cus();
     const int ksub = skinny::kWaves;  // 1-chunk tiles: the four waves share the k range
     // (measured at K <= 5120 and up to CUs / 8 leftover chunks; a longer K or
     // more leftover work per CU keeps the split tiles)
-    if (chunks >= cus && (chunks - cus) * 8 <= cus && groups >= ksub && k <= 5120 && (m <= 3 || chunks - cus <= 4)) {
-      const int64_t left = chunks - cus;
+    const int64_t per = std::min<int64_t>(chunks / cus, LB_MIXED_MAX_PER_CU), whole = per * cus;
+    if (per >= 1 && (chunks - whole) * 8 <= cus && groups >= ksub && k <= 5120 && (m <= 3 || chunks - whole <= 4)) {
+      const int64_t left = chunks - whole;
       const int s = left > 0 ? (int)std::min<int64_t>(std::min<int64_t>(cus / left, groups / ksub), 256) : 1;
       if (left == 0 || (s >= 2 && workspace_len >= 1 + chunks)) {
         pl.skinny = true;
@@ -332,7 +339,7 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
         pl.mr = 1;
         pl.cpw = 1;
         pl.n_cg = (int)chunks;
-        pl.whole = (int)cus;
+        pl.whole = (int)whole;
         pl.splits = s;
         pl.x_bytes = (size_t)groups * 128 * (size_t)m * 2;
         pl.lds = std::max(pl.x_bytes + 16, (size_t)m * skinny::kCols * 4);

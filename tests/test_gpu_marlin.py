@@ -126,12 +126,16 @@ def test_wide_decode_vs_oracle(dev, m, k, group):
     (3, 5120, 17408, 128),
     (4, 2048, 16640, 128),
     (4, 5120, 16384, 128),
+    (1, 5120, 34816, 128),
+    (2, 4096, 32768, 128),
+    (3, 5120, 33280, 128),
 ])
 def test_wide_decode_leftovers_vs_oracle(dev, m, k, n, group):
     """Decode at N just above 64 columns per CU (16384): 256-column tiles that
     do not divide evenly over the CUs, up to M = 8, both scale modes, and
     repeated launches bit-identical.  The grouped cases at M <= 4 take the
-    mixed plan (one whole-K single-chunk tile per CU, leftover chunks split)."""
+    mixed plan (one or two whole-K single-chunk tiles per CU, leftover chunks
+    split)."""
     print_case("wide-left", m, k, n, group)
     codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=900 + m + k + n)
     got = _run_gemm(dev, x, qw, sp, group)
