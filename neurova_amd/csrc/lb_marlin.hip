@@ -320,7 +320,10 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
   // 4-chunk tiles (`allow_mixed` false).  At M = 2 and 3 (N = 17408) it measured
   // 12.6 / 12.8 against 13.8 / 13.9 us; at M = 4 it gains where at most 4 chunks
   // are left over (N = 16384: 12.5 against 13.6 us; K = 2048, N = 16640: 9.2
-  // against 10.1 us) and loses with 16 (N = 17408: 14.2 against 13.9 us).
+  // against 10.1 us); with 16 left over it loses on 10 leftover splits (N = 17408:
+  // 14.2 against 13.9 us) and 4 (14.9 against 13.4) but gains on 6 (13.2 against
+  // 13.4 us; gate/up, N = 34816: 20.2 against 22.1 us), so M >= 4 caps the
+  // leftover splits at 6.
   // Two whole-K tiles per CU where the chunks number two to 2 1/8 per CU
   // (gate/up, N = 34816: 21.2 against 21.9 us; N = 33280: 19.6 against 21.4;
   // K = 4096, N = 32768: 15.5 against 16.8 us); more per CU is not measured.
@@ -330,9 +333,9 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
     // (measured at K <= 5120 and up to CUs / 8 leftover chunks; a longer K or
     // more leftover work per CU keeps the split tiles)
     const int64_t per = std::min<int64_t>(chunks / cus, LB_MIXED_MAX_PER_CU), whole = per * cus;
-    if (per >= 1 && (chunks - whole) * 8 <= cus && groups >= ksub && k <= 5120 && (m <= 3 || chunks - whole <= 4)) {
+    if (per >= 1 && (chunks - whole) * 8 <= cus && groups >= ksub && k <= 5120) {
       const int64_t left = chunks - whole;
-      const int s = left > 0 ? (int)std::min<int64_t>(std::min<int64_t>(cus / left, groups / ksub), 256) : 1;
+      const int s = left > 0 ? (int)std::min<int64_t>(std::min<int64_t>(cus / left, groups / ksub), m >= 4 ? 6 : 256) : 1;
       if (left == 0 || (s >= 2 && workspace_len >= 1 + chunks)) {
         pl.skinny = true;
         pl.direct = false;

@@ -123,10 +123,11 @@ def test_fused_mlp_model_shape_one_launch(dev, batch):
     print_case("mlp_fused_model", batch, "launches", launches)
     # from batch 5: the two launches take direct-A and ring tiles the one-launch
     # kernel does not have, so mode 1 runs them too (the gate_up launch storing
-    # the gated activations; the output stays bit-identical).  At batch 1-3 the
+    # the gated activations; the output stays bit-identical).  At batch 1-4 the
     # gate_up call plans whole-K single-chunk tiles (two per CU, leftovers
-    # split), which the one launch does not have either.
-    assert launches == (1 if batch == 4 else 2)
+    # split), which the one launch does not have either; the one launch is
+    # covered at the smaller shapes above and at 4096 x 14336 below.
+    assert launches == 2
     # auto: always the two launches (the one launch is opt-in)
     assert capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128) == 2
     args = _problem_dev(HIDDEN, INTER, batch, 7 + batch, dev)
@@ -228,7 +229,9 @@ def test_fused_mlp_give_up_is_reported_and_recovers(dev):
     import langburst_cuda as lc
     from neurova_amd import capi
 
-    batch = 4
+    # a shape whose two calls plan the staged tiles the one launch mirrors
+    batch, HIDDEN, INTER = 4, 4096, 14336
+    assert capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128, capi.MLP_ONE_LAUNCH) == 1
     print_case("mlp_fused_give_up", batch)
     x, gu_q, gu_s, d_q, d_s = _problem_dev(HIDDEN, INTER, batch, 77, dev)
     two, _ = _two_launches(dev, x, gu_q, gu_s, d_q, d_s, HIDDEN, INTER, 128, 128)

@@ -54,7 +54,7 @@ def test_plan_invariants(L, variant):
             # mixed: one whole-K single-chunk tile per CU, the leftover chunks split s ways
             whole = min(chunks // cus, 2) * cus  # one or two whole-K tiles per CU
             assert p["form"] == "staged" and cus < chunks and (chunks - whole) * 8 <= cus and k <= 5120, what
-            assert m <= 3 or chunks - whole <= 4, what
+            assert m <= 3 or s <= 6, what  # M = 4: at most 6 leftover splits
             assert p["workgroups"] == whole + (chunks - whole) * s, what
         else:
             assert p["workgroups"] == (n // (64 * cpw)) * s, what
@@ -80,15 +80,17 @@ def test_plan_rules_at_baseline_shapes(L):
     assert (p["form"], p["chunks_or_row_blocks"], p["splits"], p["workgroups"]) == ("staged", 1, 10, 416)
     p = _plan(1, 16384, 5120)
     assert (p["form"], p["chunks_or_row_blocks"], p["splits"], p["workgroups"]) == ("staged", 1, 1, 256)
-    # M = 2 and 3 take the mixed plan too; M = 4 only with at most 4 leftover chunks
+    # M = 2 and 3 take the mixed plan too; M = 4 with at most 6 leftover splits
     for m in (2, 3):
         assert _plan(m, 17408, 5120)["workgroups"] == 416
+    p = _plan(4, 17408, 5120)
+    assert (p["form"], p["chunks_or_row_blocks"], p["splits"], p["workgroups"]) == ("staged", 1, 6, 256 + 16 * 6)
     assert _plan(4, 16384, 5120)["workgroups"] == 256 and _plan(4, 16640, 2048)["workgroups"] == 256 + 4 * 4
     # gate/up (N = 34816): two whole-K tiles per CU, the 32 leftover chunks split 8 ways
     p = _plan(1, 34816, 5120)
     assert (p["form"], p["chunks_or_row_blocks"], p["splits"], p["workgroups"]) == ("staged", 1, 8, 768)
-    # M = 4 at N = 17408 and K = 17408 keep the split 4-chunk tiles
-    assert (_plan(4, 17408, 5120)["chunks_or_row_blocks"], _plan(1, 17408, 17408)["chunks_or_row_blocks"]) == (4, 4)
+    # K = 17408 keeps the split 4-chunk tiles
+    assert _plan(1, 17408, 17408)["chunks_or_row_blocks"] == 4
     # narrow decode projections take 64-column direct tiles
     for m in (1, 4, 16):
         assert _plan(m, 7168, 5120)["form"] == "direct"
