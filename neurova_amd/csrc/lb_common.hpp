@@ -126,6 +126,8 @@ __device__ __forceinline__ __amdgpu_buffer_rsrc_t buffer_of(const void* base, ui
 // through a buffer resource (cache-policy operand 16 = sc1 on gfx950), for
 // hand-offs of whole accumulator registers.
 constexpr int kSc1 = 16;
+// Cache-policy operand 2 = nt on gfx950: data read once (weights, scales).
+constexpr int kNonTemporal = 2;
 __device__ __forceinline__ void publish16(__amdgpu_buffer_rsrc_t r, uint32_t off, f32x4 v) {
   __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), r, off, 0, kSc1);
 }

@@ -454,9 +454,11 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   if (var == V_ARGMAX ? (!argmax_state || !argmax_out) : !c) return LB_ERR_ARG;
   if (!lbh::aligned(a, 16) || !lbh::aligned(b, 16) || !lbh::aligned(s, 16) || (c && !lbh::aligned(c, 2)))
     return LB_ERR_ALIGN;
-  // The GEMM kernel addresses A, B and s through 32-bit buffer resources.
+  // The GEMM kernel addresses A, B and s through 32-bit buffer resources, the
+  // decode kernel B and s with 32-bit offsets.
   const int64_t a_bytes = m * k * 2 * (var == V_SILU ? 2 : 1);
   if (m > skinny::kMaxM && (a_bytes >= (1LL << 31) || k * n / 2 >= (1LL << 31))) return LB_ERR_PROB_SHAPE;
+  if (k * n / 2 >= (1LL << 32)) return LB_ERR_PROB_SHAPE;
   const bool gated = var == V_SILU || var == V_SILU_DONE;
   const Plan pl = make_plan(m, n, k, workspace_len, gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, var == V_ARGMAX,
                             true, grouped != 0);

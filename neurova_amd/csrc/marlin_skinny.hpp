@@ -325,7 +325,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   // dependent ones: the split fields, a division, then the pointers).
   asm volatile("" ::"s"(p.a), "s"(p.b), "s"(p.s), "s"(p.m), "s"(p.n), "s"(p.k), "s"(p.splits), "s"(p.kp_total));
   const int tid = threadIdx.x;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the ring's offsets stay scalar
   const int lane = tid & 63;
   const int mrows = p.m;      // <= kRows
   constexpr int cpw = CPW;
@@ -345,7 +345,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
 
   // fragment coordinates: lane = 16g + 8h + c
   const int chunk = EPI == EPI_ACT ? tile_chunk<EPI, CPW>(p, cg, wchunk) : cg * cpw + wchunk;
-  const int64_t row_words = 2 * (int64_t)p.n;  // int32 per qweight row
+  const uint32_t row_bytes = (uint32_t)p.n * 8u;  // one qweight row: 2N int32
   const int g = lane >> 4;
   const int hsel = (lane >> 3) & 1;
   const int cc = lane & 7;
@@ -353,8 +353,17 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   const int gq = g & 1;     // slot pair (q0, q1) = (2gq, 2gq+1)
   // Each lane loads one slot, 4c + 2gq + h; the pair's other slot comes from
   // lane ^ 8 (same c and g, other h) by a DPP row rotation.
-  const uint32_t* bsrc = p.b + (int64_t)prow * row_words + (int64_t)chunk * 128 + (cc * 4 + gq * 2 + hsel) * 4;
-  const uint16_t* ssrc = p.s + chunk * 64 + cc * 8;
+  // The lane's offset into the weights and scales is a fixed 32-bit VGPR and
+  // each step's row offset a wave-uniform scalar (32-bit: the host keeps the
+  // weights below 4 GB), so the ring costs two VALU per 16-byte load instead
+  // of a 64-bit multiply-add.  Weights and scales are read once: non-temporal
+  // loads.  The scales come through a buffer descriptor (with the weights as
+  // buffer loads too, the compiler drains the ring at the loop head).
+  const __amdgpu_buffer_rsrc_t rbs = buffer_of(p.s, (uint32_t)(p.k >> 7) * (uint32_t)p.n * 2u);
+  const uint32_t bvoff = (uint32_t)prow * row_bytes + (uint32_t)chunk * 512u + (uint32_t)(cc * 4 + gq * 2 + hsel) * 16u;
+  const uint32_t svoff = (uint32_t)chunk * 128u + (uint32_t)cc * 16u;
+  const uint32_t step_bytes = 2u * row_bytes;      // one 32-k step: two qweight rows
+  const uint32_t group_bytes = (uint32_t)p.n * 2u;  // one row of group scales
   // Byte selection of v_perm_b32(own, partner): word = [A.b_h, B.b_h, A.b_(2+h), B.b_(2+h)]
   // with A = slot 4c+2gq (q0) and B = slot 4c+2gq+1 (q1).
   const uint32_t psel = hsel ? 0x07030501u : 0x02060004u;
@@ -369,6 +378,11 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   const int octs = nkp * 4;            // 8-half runs per row of the slice
   const int items = octs * mrows;
   const int n_frag = nkp * 4 * mrows;  // staged entries; afr[n_frag] is the zero entry
+  // Item it is octet it % octs of row it / octs.  The staged slice fits LDS, so
+  // it and octs stay below 2^16, where umulhi(it, ceil(2^32 / octs)) is exactly
+  // it / octs (the error term it * (ceil(2^32 / octs) * octs - 2^32) / 2^32 < 1 / octs
+  // never reaches the next integer); octs >= 16.
+  const uint32_t oct_magic = 0xffffffffu / (uint32_t)octs + 1u;
   const int64_t a_row_stride = AM == A_SILU_PACKED ? 2 * (int64_t)p.k : (int64_t)p.k;
   const __amdgpu_buffer_rsrc_t ra = buffer_of(p.a, (uint32_t)((int64_t)mrows * p.k * 2));  // A_HANDOFF
   uint4 gv[kStageUnroll], uv[kStageUnroll];
@@ -376,8 +390,9 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
 #pragma unroll
     for (int u = 0; u < kStageUnroll; ++u) {
       const int it = min(base + u * kThreads + tid, items - 1);
-      const int mm = it / octs;
-      const uint16_t* src = p.a + (int64_t)mm * a_row_stride + k0 + ((it - mm * octs) << 3);
+      const int mm = (int)__umulhi((uint32_t)it, oct_magic);
+      const int r = it - mm * octs;
+      const uint16_t* src = p.a + (int64_t)mm * a_row_stride + k0 + (r << 3);
       if (AM == A_HANDOFF)
         gv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, (uint32_t)(src - p.a) * 2u, 0, kSc1));
       else
@@ -390,7 +405,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     for (int u = 0; u < kStageUnroll; ++u) {
       const int it = base + u * kThreads + tid;
       if (it < items) {
-        const int mm = it / octs;
+        const int mm = (int)__umulhi((uint32_t)it, oct_magic);
         const int r = it - mm * octs;  // kp = r >> 2, octet o = r & 3 = 2 prow + half
         uint4 w = gv[u];
         if (AM == A_SILU_PACKED)
@@ -455,18 +470,24 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   u32x4 aw[kDepth][kSteps][MR];  // A_DIRECT only
 #pragma unroll
   for (int i = 0; i < kDepth; ++i) bs[i] = (u32x4){0, 0, 0, 0};
-  auto issue = [&](int slot, int batch) __attribute__((always_inline)) {
+  auto issue_step = [&](int slot, int batch, int d) __attribute__((always_inline)) {
     const int kpf = kpw0 + batch * kSteps;
+    const char* base = reinterpret_cast<const char*>(p.b) + (size_t)((uint32_t)(kpf + d) * step_bytes);  // uniform
+    bw[slot][d] = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(base + bvoff));
+    if constexpr (kDirect) {
 #pragma unroll
-    for (int d = 0; d < kSteps; ++d) {
-      const u32x4* src = reinterpret_cast<const u32x4*>(bsrc + (int64_t)(kpf + d) * 2 * row_words);
-      bw[slot][d] = *src;
-      if constexpr (kDirect) {
-#pragma unroll
-        for (int rb = 0; rb < MR; ++rb) aw[slot][d][rb] = *reinterpret_cast<const u32x4*>(arow[rb] + 32 * (kpf + d));
-      }
+      for (int rb = 0; rb < MR; ++rb) aw[slot][d][rb] = *reinterpret_cast<const u32x4*>(arow[rb] + 32 * (kpf + d));
     }
-    if (GROUPED) bs[slot] = *reinterpret_cast<const u32x4*>(ssrc + (int64_t)(kpf >> 2) * p.n);
+  };
+  auto issue_scale = [&](int slot, int batch) __attribute__((always_inline)) {
+    const int kpf = kpw0 + batch * kSteps;
+    if (GROUPED)
+      bs[slot] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rbs, svoff, (uint32_t)(kpf >> 2) * group_bytes, kNonTemporal));
+  };
+  auto issue = [&](int slot, int batch) __attribute__((always_inline)) {
+#pragma unroll
+    for (int d = 0; d < kSteps; ++d) issue_step(slot, batch, d);
+    issue_scale(slot, batch);
   };
 
   // ---- staging loads, then the first weight batches, then the stores ----
