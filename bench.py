@@ -164,13 +164,12 @@ class DecodeStep:
     17408->5120 through the SiLU-gated op on that `mixed` row -- the
     production call sequence (langburst/model.py:1414-1482).  W4 g128 random
     packed weights, all resident (about 10.9 GB).  fused_mlp: gate/up, SiLU
-    and down as one lb_marlin_mlp_fused call asking for one launch (mode 1: one
-    launch where both projections plan the same tiles as the two calls, here
-    M <= 4; at M = 16 and 32 two launches, gate/up tiles storing
-    fp16(silu(g) * u) and then down over those activations), whose output is
-    bit-identical to the two calls.  A call is one op of the C ABI; the
-    SiLU-gated down projection at M >= 5 is two kernel launches (the gated
-    activations first)."""
+    and down as one lb_marlin_mlp_fused call (at M = 16 and 32 its gate/up
+    launch stores fp16(silu(g) * u) and the down launch reads those
+    activations, instead of the [gate | up] row and the gated op's own
+    pre-pass), whose output is bit-identical to the two calls.  A call is one
+    op of the C ABI; the SiLU-gated down projection at M >= 5 is two kernel
+    launches (the gated activations first)."""
 
     HIDDEN, INTER, QKV, O_IN = 5120, 17408, 7168, 5120
 
@@ -203,7 +202,7 @@ class DecodeStep:
             self.fws = torch.zeros((capi.marlin_mlp_fused_workspace_len(m, h, it),), dtype=torch.int32, device=dev)
             self.fscratch = torch.empty((capi.marlin_mlp_fused_scratch_bytes(m, h, it),), dtype=torch.uint8,
                                         device=dev)
-            self.calls_per_layer = 2 + capi.marlin_mlp_fused_launches(m, h, it, 128, 128, capi.MLP_ONE_LAUNCH)
+            self.calls_per_layer = 3
         per_layer = (marlin_bytes(m, h, self.QKV) + marlin_bytes(m, self.O_IN, h) + marlin_bytes(m, h, 2 * it)
                      + marlin_bytes(m, it, h) + m * it * 2)  # the gated op reads [gate | up]: 2K halves per row
         self.bytes_per_step = per_layer * layers
@@ -216,11 +215,75 @@ class DecodeStep:
             lc.lowbit_marlin_gemm_out(*L["o"], self.x, self.o_out, self.ws, self.O_IN, 128)
             if self.fused_mlp:
                 st = self.capi.marlin_mlp_fused(self.x, *L["gate_up"], *L["down"], self.down_out, h, it, 128, 128,
-                                                self.fws, self.fscratch, mode=self.capi.MLP_ONE_LAUNCH)
+                                                self.fws, self.fscratch)
                 assert st == 0, self.capi.status_string(st)
             else:
                 lc.lowbit_marlin_gemm_out(*L["gate_up"], self.x, self.mixed, self.ws, h, 128)
                 lc.lowbit_marlin_gemm_silu_packed_out(*L["down"], self.mixed, self.down_out, self.ws, it, 128)
+
+
+# The projections the reference publishes M = 1 timings for
+# (langburst/docs/PERFORMANCE_LOG.md:421-427, RTX 4080 16GB), K x N.  Those
+# figures are another GPU's and are reported beside this device's only as
+# context; vs_baseline stays null.
+PUBLISHED_M1 = [
+    ("mlp_gate_up", 5120, 34816, 150.87),
+    ("mlp_down", 17408, 5120, 73.90),
+    ("gdn_qkvz", 5120, 16384, 69.79),
+    ("gdn_out", 6144, 5120, 40.00),
+    ("attn_qkv", 5120, 14336, 61.92),
+    ("attn_o", 6144, 5120, 39.85),
+]
+LM_HEAD = ("lm_head_argmax", 5120, 248320, 988.42)
+
+
+def published_projections(torch, lc, dev, use_graph):
+    """M = 1 calls of the reference's published projection shapes (plain
+    Marlin GEMM, rotating weight sets > 2x the Infinity Cache) and the lm_head
+    fused argmax (5120 -> 248320, two weight sets of 656 MB each)."""
+    from neurova_amd import capi
+
+    res = {"reference_source": "langburst/docs/PERFORMANCE_LOG.md:421-427 (RTX 4080 16GB, M = 1)"}
+    done = {}
+    for name, k, n, ref_us in PUBLISHED_M1:
+        if (k, n) not in done:
+            pc = marlin_bytes(1, k, n)
+            ns = sets_for(pc)
+            pr = MarlinProblem(torch, dev, 1, k, n, ns, seed=30 + k % 97 + n % 89)
+            ms2, _, nc2 = time_calls(torch, lambda i: pr.call(lc, i), ns, calls_per_step_for(ns, 600), 5, use_graph)
+            done[(k, n)] = (ms2 * 1e3 / nc2, pc)
+            del pr
+        u, pc = done[(k, n)]
+        res[name] = {"k": k, "n": n, "us_per_call": round(u, 3), "GB/s": round(pc / u / 1e3, 1),
+                     "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4), "reference_rtx4080_us": ref_us}
+        log(f"[bench] published {name} K={k} N={n}: {u:.2f} us, {pc / u / 1e3:.1f} GB/s")
+    name, k, n, ref_us = LM_HEAD
+    pc = marlin_bytes(1, k, n)
+    ns = 2
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(40)
+    qs = [torch.randint(-2 ** 31, 2 ** 31, (k // 16, 2 * n), dtype=torch.int32, device=dev, generator=gen)
+          for _ in range(ns)]
+    ss = [(torch.randn((k // 128, n), device=dev, generator=gen) * 0.01).abs_().add_(1e-3).half() for _ in range(ns)]
+    x = torch.randn((1, k), device=dev, generator=gen).half()
+    ws = torch.zeros((n // 128 * 16,), dtype=torch.int32, device=dev)
+    state = torch.zeros((1,), dtype=torch.int64, device=dev)
+    out = torch.zeros((1,), dtype=torch.int64, device=dev)
+    sync = torch.zeros((2,), dtype=torch.int32, device=dev)
+    sc = torch.empty((max(1, capi.marlin_scratch_bytes(1, n, k, 128)),), dtype=torch.uint8, device=dev)
+
+    def call(i):
+        assert capi.marlin_gemm_argmax(x, qs[i], ss[i], ws, 128, state, out, sync, 1, sc) == 0
+
+    ms2, _, nc2 = time_calls(torch, call, ns, 50, 5, use_graph)
+    u = ms2 * 1e3 / nc2
+    res[name] = {"k": k, "n": n, "us_per_call": round(u, 3), "GB/s": round(pc / u / 1e3, 1),
+                 "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4), "reference_rtx4080_us": ref_us,
+                 "bytes_per_call": pc}
+    log(f"[bench] lm_head argmax K={k} N={n}: {u:.2f} us, {pc / u / 1e3:.1f} GB/s")
+    del qs, ss
+    torch.cuda.empty_cache()
+    return res
 
 
 def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5, fused_mlp=False):
@@ -253,9 +316,6 @@ def decode_step_sweep(torch, lc, dev, m, layers=64, replays=5, fused_mlp=False):
            "bytes_per_step": ds.bytes_per_step, "weight_bytes_resident": ds.weight_bytes,
            "GB/s": round(ds.bytes_per_step / us / 1e3, 1),
            "frac_hbm": round(ds.bytes_per_step / us / 1e3 / HBM_PEAK_GBS, 4)}
-    if fused_mlp:  # the one-launch form's in-kernel waits must not have given up
-        st = ds.capi.marlin_mlp_fused_check(ds.fws)
-        res["one_launch_check"] = "ok" if st == 0 else ds.capi.status_string(st)
     del graph, ds
     torch.cuda.empty_cache()
     return res
@@ -426,10 +486,9 @@ def gemm_probe(torch, lc, dev, calls=6):
 def mlp_probe(torch, dev, calls=40):
     """The production MLP at the model's shape (hidden 5120, intermediate
     17408, W4 g128) for M = 1, 4, 16, 32: `calls` graph-replayed calls of the
-    two reference ops and of lb_marlin_mlp_fused (mode 1: one launch where its
-    tiles match the two ops', M <= 4; otherwise its two-launch form, whose
-    gate_up launch stores the gated activations), over 4 rotating weight sets,
-    for the kernel-trace runs."""
+    two reference ops and of lb_marlin_mlp_fused (from M = 5 its gate_up launch
+    stores the gated activations), over 4 rotating weight sets, for the
+    kernel-trace runs."""
     from neurova_amd import capi
 
     h, it, sets = DecodeStep.HIDDEN, DecodeStep.INTER, 4
@@ -459,8 +518,7 @@ def mlp_probe(torch, dev, calls=40):
 
         def fused(i):
             (gq, gs), (dq, ds) = w[i % sets]
-            assert capi.marlin_mlp_fused(x, gq, gs, dq, ds, out, h, it, 128, 128, ws, fsc,
-                                         mode=capi.MLP_ONE_LAUNCH) == 0
+            assert capi.marlin_mlp_fused(x, gq, gs, dq, ds, out, h, it, 128, 128, ws, fsc) == 0
 
         accum = torch.empty((m, h), dtype=torch.float32, device=dev)
         sync = torch.zeros((2 * m,), dtype=torch.int32, device=dev)
@@ -470,7 +528,7 @@ def mlp_probe(torch, dev, calls=40):
             (gq, gs), (dq, ds) = w[i % sets]
             assert capi.marlin_mlp_streaming(gq, gs, dq, ds, x, out, accum, sync, h, it, 128, 128, ssc) == 0
 
-        for name, fn, n_calls in (("two reference ops", pair, calls), ("lb_marlin_mlp_fused mode 1", fused, calls),
+        for name, fn, n_calls in (("two reference ops", pair, calls), ("lb_marlin_mlp_fused", fused, calls),
                                   ("streaming (fp32 numerics)", streaming, sets)):
             ms, _, nc = time_calls(torch, fn, sets, calls_per_step_for(sets, n_calls), 1, True)
             log(f"[mlp-probe] M={m:2d} {name}: {ms * 1e3 / nc:.2f} us per MLP")
@@ -490,7 +548,7 @@ def main():
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true", help="run the counter-calibration probe and exit")
     ap.add_argument("--gemm-probe", action="store_true", help="run the prefill GEMM counter probe and exit")
-    ap.add_argument("--mlp-probe", action="store_true", help="time the decode MLP (two launches / one launch) and exit")
+    ap.add_argument("--mlp-probe", action="store_true", help="time the decode MLP (the reference op pair / lb_marlin_mlp_fused) and exit")
     ap.add_argument("--stream-probe", action="store_true",
                     help="time the streaming-read ceiling over the headline's bytes (or --stream-mb) and exit")
     ap.add_argument("--stream-mb", default="", help="comma-separated MB (1e6 bytes) for --stream-probe")
@@ -587,6 +645,7 @@ def main():
                                            "frac_hbm": round(pc / u / 1e3 / HBM_PEAK_GBS, 4)}
             log(f"[bench] M={mm}: {u:.2f} us, {pc / u / 1e3:.1f} GB/s")
             del pr
+        extra["published_projections_m1"] = published_projections(torch, lc, dev, use_graph)
         for (kk, nn) in ((5120, 17408), (17408, 5120)):
             mm = 2048
             pr = MarlinProblem(torch, dev, mm, kk, nn, 2, seed=11)
@@ -647,9 +706,9 @@ def main():
         for mm in (1, 4, 16, 32):
             extra[f"decode_step_64_layers_m{mm}"] = r = decode_step_sweep(torch, lc, dev, mm)
             log(f"[bench] 64-layer decode step M={mm}: {r['us_per_step']:.1f} us, {r['GB/s']:.1f} GB/s")
-        for mm in (4, 16, 32):
+        for mm in (16, 32):
             extra[f"decode_step_64_layers_m{mm}_fused_mlp"] = r = decode_step_sweep(torch, lc, dev, mm, fused_mlp=True)
-            log(f"[bench] 64-layer decode step M={mm}, lb_marlin_mlp_fused mode 1: {r['us_per_step']:.1f} us, "
+            log(f"[bench] 64-layer decode step M={mm}, lb_marlin_mlp_fused: {r['us_per_step']:.1f} us, "
                 f"{r['calls_per_step']} calls")
         result["extra"] = extra
 

@@ -36,7 +36,7 @@ enum lb_status {
   LB_ERR_WORKSPACE = 5,  /* workspace shorter than required */
   LB_ERR_SCRATCH = 6,    /* scratch buffer shorter than lb_marlin_scratch_bytes() */
   LB_ERR_HIP = 7,        /* the HIP runtime reported an error at launch */
-  LB_ERR_HANDOFF = 8,    /* lb_marlin_mlp_fused_check: an in-kernel wait gave up (output not valid) */
+  /* 8 is not used */
   LB_ERR_NOALLOC_LIMIT = 9 /* lb_marlin_gemm_noalloc: the problem needs more than its static scratch */
 };
 
@@ -178,49 +178,31 @@ int lb_marlin_mlp_streaming(const int32_t* gate_up_qweight, const uint16_t* gate
  * reference's production MLP, which runs the gate_up projection and then
  * down.gemm_silu_packed as two launches (adapters/qwen36_impl/model.py:1460-1470
  * _fused_marlin_down, loader.py:337-368): bit-identical to lb_marlin_gemm followed
- * by lb_marlin_gemm_silu_packed, in every mode.
+ * by lb_marlin_gemm_silu_packed.  Two launches as well; where the gate_up
+ * projection plans decode tiles of 2 or 4 chunks, its launch pairs the gate and
+ * up chunks of the same neurons and stores fp16(silu(g) * u) instead of [g | u].
  * No reference op: replaces that pair of calls.
- * mode: 0 auto and 2: the two launches; 1: one launch when every workgroup
- *       of it fits on the device at once (else the two launches).  The one
- *       launch hands activations between workgroups with bounded waits that
- *       need all of its workgroups resident; a wait that gives up (another
- *       kernel holding compute units) leaves that call's output not valid,
- *       so it runs only when the caller asks for it and checks the call with
- *       lb_marlin_mlp_fused_check.  lb_marlin_mlp_fused_launches says which
- *       form a call takes.
- * workspace: int32 [lb_marlin_mlp_fused_workspace_len()], zero on entry, left
- *            zero (entry 1 stays 1 if a one-launch wait gave up).
+ * workspace: int32 [lb_marlin_mlp_fused_workspace_len()], zero on entry, left zero.
  * scratch:   lb_marlin_mlp_fused_scratch_bytes() bytes, 256-byte aligned.
- * Calls that share a workspace must not overlap. */
+ * Calls that share a workspace or scratch must not overlap. */
 size_t lb_marlin_mlp_fused_scratch_bytes(int64_t batch, int64_t hidden, int64_t intermediate);
 int64_t lb_marlin_mlp_fused_workspace_len(int64_t batch, int64_t hidden, int64_t intermediate);
-/* 1 (one launch), 2 (two launches), 0 (batch 0) or -status for an unsupported problem or mode. */
-int lb_marlin_mlp_fused_launches(int64_t batch, int64_t hidden, int64_t intermediate,
-                                 int64_t gate_group_size, int64_t down_group_size, int32_t mode);
 int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qweight, const uint16_t* gate_up_scales,
                         const int32_t* down_qweight, const uint16_t* down_scales, uint16_t* out,
                         int64_t batch, int64_t hidden, int64_t intermediate,
-                        int64_t gate_group_size, int64_t down_group_size, int32_t mode,
+                        int64_t gate_group_size, int64_t down_group_size,
                         int32_t* workspace, int64_t workspace_len,
                         void* scratch, size_t scratch_bytes, lb_stream_t stream);
-/* Waits for `stream`, then reads the workspace of lb_marlin_mlp_fused calls:
- * LB_ERR_HANDOFF if a one-launch wait gave up since the workspace was last
- * checked (the workspace, workspace_len entries, is then zeroed, so the next
- * call starts clean), else LB_OK.  Synchronises; no reference counterpart. */
-int lb_marlin_mlp_fused_check(int32_t* workspace, int64_t workspace_len, lb_stream_t stream);
-/* Test hook: polls a one-launch wait makes before it gives up (default
- * 262144; values < 1 restore the default).  Lets a test force the give-up
- * path from the host with every kernel still ending normally. */
-void lb_marlin_mlp_fused_set_spin_limit(int32_t polls);
 
 /* lb_marlin_gemm without caller scratch and without any allocation: no
  * counterpart in the reference; for callers that cannot allocate (code under
  * HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  * The split-K partials go to a static device array of
- * lb_marlin_noalloc_scratch_limit() bytes (32 MiB) that each GPU holds until
+ * lb_marlin_noalloc_scratch_limit() bytes (64 MiB) that each GPU holds until
  * the process ends; problems whose plan needs more return
  * LB_ERR_NOALLOC_LIMIT before anything is launched (every decode shape up to
- * M = 64 of the BASELINE.json projections fits; M = 2048 prefill does not).  All
+ * M = 64 of the BASELINE.json projections and of the reference's published
+ * ones, lm_head 5120 -> 248320 included, fits; M = 2048 prefill does not).  All
  * calls on one GPU share that array: calls that overlap (other streams) race
  * and must be serialised by the caller.  Same arguments, workspace contract
  * and results as lb_marlin_gemm. */
@@ -238,9 +220,11 @@ int lb_marlin_dequant(const int32_t* B, const uint16_t* s, uint16_t* w_nk,
 
 /* ---------------- Measurement probe (no reference counterpart) ----------------
  * Reads `bytes` (a multiple of 16) of device memory at `src` with 16-byte
- * loads over `workgroups` workgroups of 256 threads, each a contiguous range,
- * and writes one word per wave to sink[workgroups * 4]: the streaming-read
- * ceiling that the bandwidth-bound kernels are compared with. */
+ * non-temporal loads over `workgroups` workgroups of 256 threads, each a
+ * contiguous range (a ring of 8 loads in flight per lane), and folds the data
+ * into one word per workgroup, stored to sink[workgroup] only when it equals a
+ * fixed value (sink holds `workgroups` words): the streaming-read ceiling that
+ * the bandwidth-bound kernels are compared with. */
 int lb_probe_stream_read(const void* src, size_t bytes, uint32_t* sink, int32_t workgroups, lb_stream_t stream);
 
 #ifdef __cplusplus

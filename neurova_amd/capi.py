@@ -24,7 +24,6 @@ LB_ERR_ALIGN = 4
 LB_ERR_WORKSPACE = 5
 LB_ERR_SCRATCH = 6
 LB_ERR_HIP = 7
-LB_ERR_HANDOFF = 8
 LB_ERR_NOALLOC_LIMIT = 9
 
 P = ctypes.c_void_p
@@ -52,10 +51,7 @@ _SIGNATURES = {
     "lb_marlin_gemm_noalloc": ([P, P, P, P, I64, I64, I64, P, I64, I64, P], ctypes.c_int),
     "lb_marlin_mlp_fused_scratch_bytes": ([I64, I64, I64], SZ),
     "lb_marlin_mlp_fused_workspace_len": ([I64, I64, I64], I64),
-    "lb_marlin_mlp_fused_launches": ([I64, I64, I64, I64, I64, I32], ctypes.c_int),
-    "lb_marlin_mlp_fused": ([P, P, P, P, P, P, I64, I64, I64, I64, I64, I32, P, I64, P, SZ, P], ctypes.c_int),
-    "lb_marlin_mlp_fused_check": ([P, I64, P], ctypes.c_int),
-    "lb_marlin_mlp_fused_set_spin_limit": ([I32], None),
+    "lb_marlin_mlp_fused": ([P, P, P, P, P, P, I64, I64, I64, I64, I64, P, I64, P, SZ, P], ctypes.c_int),
 }
 
 
@@ -184,27 +180,11 @@ def marlin_mlp_fused_workspace_len(batch, hidden, intermediate) -> int:
     return int(lib().lb_marlin_mlp_fused_workspace_len(batch, hidden, intermediate))
 
 
-MLP_AUTO, MLP_ONE_LAUNCH, MLP_TWO_LAUNCHES = 0, 1, 2
-
-
-def marlin_mlp_fused_launches(batch, hidden, intermediate, gg, dg, mode=MLP_AUTO) -> int:
-    return int(lib().lb_marlin_mlp_fused_launches(batch, hidden, intermediate, gg, dg, mode))
-
-
-def marlin_mlp_fused(x, gu_q, gu_s, d_q, d_s, out, hidden, intermediate, gg, dg, workspace, scratch,
-                     mode=MLP_AUTO) -> int:
+def marlin_mlp_fused(x, gu_q, gu_s, d_q, d_s, out, hidden, intermediate, gg, dg, workspace, scratch) -> int:
     nbytes = scratch.numel() * scratch.element_size()
     return lib().lb_marlin_mlp_fused(_ptr(x), _ptr(gu_q), _ptr(gu_s), _ptr(d_q), _ptr(d_s), _ptr(out), x.shape[0],
-                                     hidden, intermediate, gg, dg, mode, _ptr(workspace), workspace.numel(),
+                                     hidden, intermediate, gg, dg, _ptr(workspace), workspace.numel(),
                                      _ptr(scratch), nbytes, _stream(x))
-
-
-def marlin_mlp_fused_check(workspace) -> int:
-    return lib().lb_marlin_mlp_fused_check(_ptr(workspace), workspace.numel(), _stream(workspace))
-
-
-def marlin_mlp_fused_set_spin_limit(polls: int) -> None:
-    lib().lb_marlin_mlp_fused_set_spin_limit(int(polls))
 
 
 def marlin_dequant(b, s, w_nk, k, group_size) -> int:

@@ -12,8 +12,13 @@
 #include <c10/hip/HIPStream.h>
 #include <c10/core/DeviceGuard.h>
 
+#include <hip/hip_runtime_api.h>
+
 #include <cstdlib>
+#include <map>
+#include <mutex>
 #include <string>
+#include <utility>
 #include <vector>
 
 #include "../../include/langburst_lowbit.h"
@@ -161,9 +166,49 @@ MarlinShape check_marlin_common(const torch::Tensor& qweight, const torch::Tenso
   return {prob_m, prob_n, prob_k, groupsize};
 }
 
-torch::Tensor scratch_for(int64_t m, int64_t n, int64_t k, int64_t g, const torch::Tensor& like) {
-  const size_t bytes = lb_marlin_scratch_bytes(m, n, k, g);
-  return torch::empty({(int64_t)std::max<size_t>(bytes, 1)}, like.options().dtype(torch::kUInt8));
+// Device scratch (split-K partials, argmax keys, the MLP's activations) for
+// the ops below.  The reference's _out ops take every buffer from the caller
+// and allocate nothing; here each (device, stream) keeps one buffer, grown on
+// demand (the caching allocator's stream ordering makes the swap safe for
+// launches already queued on that stream), so that repeated calls allocate
+// nothing.  Calls on one stream run in order and may share it.  A call under
+// HIP graph capture takes a buffer of its own from the capture's pool instead
+// (baked into the graph, so replays allocate nothing either), which keeps
+// graphs independent of the eager buffer and of each other.
+struct OpScratch {
+  torch::Tensor hold;  // keeps a capture-time buffer alive until the launch is queued
+  void* ptr = nullptr;
+  size_t bytes = 0;
+};
+
+OpScratch op_scratch(size_t bytes, const torch::Tensor& like) {
+  OpScratch r;
+  if (bytes == 0) return r;
+  const hipStream_t st = reinterpret_cast<hipStream_t>(stream_of(like));
+  hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+  if (hipStreamIsCapturing(st, &cap) != hipSuccess) cap = hipStreamCaptureStatusNone;
+  if (cap != hipStreamCaptureStatusNone) {
+    r.hold = torch::empty({(int64_t)bytes}, like.options().dtype(torch::kUInt8));
+    r.ptr = r.hold.data_ptr();
+    r.bytes = bytes;
+    return r;
+  }
+  static std::mutex mu;
+  static std::map<std::pair<int, hipStream_t>, torch::Tensor> cache;
+  std::lock_guard<std::mutex> lock(mu);
+  torch::Tensor& t = cache[{like.get_device(), st}];
+  if (!t.defined() || (size_t)t.numel() < bytes) {
+    t = torch::Tensor();
+    const size_t grown = (bytes + (1u << 20) - 1) & ~(size_t)((1u << 20) - 1);  // whole MiB
+    t = torch::empty({(int64_t)grown}, like.options().dtype(torch::kUInt8));
+  }
+  r.ptr = t.data_ptr();
+  r.bytes = (size_t)t.numel();
+  return r;
+}
+
+OpScratch scratch_for(int64_t m, int64_t n, int64_t k, int64_t g, const torch::Tensor& like) {
+  return op_scratch(lb_marlin_scratch_bytes(m, n, k, g), like);
 }
 
 void run_lowbit_marlin_gemm(torch::Tensor qweight, torch::Tensor scales, torch::Tensor x, torch::Tensor out,
@@ -180,8 +225,8 @@ void run_lowbit_marlin_gemm(torch::Tensor qweight, torch::Tensor scales, torch::
   const c10::DeviceGuard guard(x.device());
   auto scratch = scratch_for(sh.m, sh.n, sh.k, sh.group, x);
   const int err = lb_marlin_gemm(h16(x), qweight.data_ptr<int32_t>(), h16m(out), h16(scales), sh.m, sh.n, sh.k,
-                                 workspace.data_ptr<int32_t>(), workspace.numel(), sh.group, scratch.data_ptr(),
-                                 (size_t)scratch.numel(), stream_of(x));
+                                 workspace.data_ptr<int32_t>(), workspace.numel(), sh.group, scratch.ptr,
+                                 scratch.bytes, stream_of(x));
   TORCH_CHECK(err == 0, "Marlin kernel failed with code ", err);
 }
 
@@ -217,7 +262,7 @@ void lowbit_marlin_gemm_silu_packed_out(torch::Tensor qweight, torch::Tensor sca
   auto scratch = scratch_for(sh.m, sh.n, sh.k, sh.group, mixed);
   const int err = lb_marlin_gemm_silu_packed(h16(mixed), qweight.data_ptr<int32_t>(), h16m(out), h16(scales), sh.m,
                                              sh.n, sh.k, workspace.data_ptr<int32_t>(), workspace.numel(), sh.group,
-                                             scratch.data_ptr(), (size_t)scratch.numel(), stream_of(mixed));
+                                             scratch.ptr, scratch.bytes, stream_of(mixed));
   TORCH_CHECK(err == 0, "Marlin silu-packed kernel failed with code ", err);
 }
 
@@ -250,8 +295,8 @@ void lowbit_marlin_gemm_argmax_out(torch::Tensor qweight, torch::Tensor scales, 
   const int err = lb_marlin_gemm_argmax(h16(x), qweight.data_ptr<int32_t>(), h16(scales), sh.m, sh.n, sh.k,
                                         workspace.data_ptr<int32_t>(), workspace.numel(), sh.group,
                                         argmax_state.data_ptr<int64_t>(), argmax_out.data_ptr<int64_t>(),
-                                        argmax_sync.data_ptr<int32_t>(), (int32_t)argmax_epoch, scratch.data_ptr(),
-                                        (size_t)scratch.numel(), stream_of(x));
+                                        argmax_sync.data_ptr<int32_t>(), (int32_t)argmax_epoch, scratch.ptr,
+                                        scratch.bytes, stream_of(x));
   TORCH_CHECK(err == 0, "Marlin argmax kernel failed with code ", err);
 }
 
@@ -298,29 +343,24 @@ void lowbit_marlin_mlp_streaming_out(torch::Tensor gate_up_qweight, torch::Tenso
               "down scales shape mismatch");
   TORCH_CHECK(epoch > 0, "epoch must be positive");
   const c10::DeviceGuard guard(x.device());
-  const size_t bytes = lb_marlin_mlp_scratch_bytes(batch, hidden, intermediate);
-  auto scratch = torch::empty({(int64_t)std::max<size_t>(bytes, 1)}, x.options().dtype(torch::kUInt8));
+  auto scratch = op_scratch(lb_marlin_mlp_scratch_bytes(batch, hidden, intermediate), x);
   const int err = lb_marlin_mlp_streaming(gate_up_qweight.data_ptr<int32_t>(), h16(gate_up_scales),
                                           down_qweight.data_ptr<int32_t>(), h16(down_scales), h16(x), h16m(out),
                                           accum.data_ptr<float>(), sync.data_ptr<int32_t>(), batch, hidden,
-                                          intermediate, gate_group, down_group, scratch.data_ptr(),
-                                          (size_t)scratch.numel(), stream_of(x));
+                                          intermediate, gate_group, down_group, scratch.ptr, scratch.bytes,
+                                          stream_of(x));
   TORCH_CHECK(err == 0, "Marlin streaming MLP failed with code ", err, " (", lb_status_string(err), ")");
 }
 
 // The decode MLP the reference's _fused_marlin_down runs as two ops
 // (langburst/adapters/qwen36_impl/model.py:1460-1470: gate/up GEMM, then the
-// SiLU-packed down GEMM), as one call, bit-identical to the two ops.  Mode 0
-// (default) and 2 run the two launches; mode 1 runs one kernel launch where it
-// fits, whose in-kernel waits can give up when other work holds compute units
-// (the output of that call is then not valid).  check=True synchronises after
-// the call and raises RuntimeError if that happened, after zeroing the
-// workspace so that the next call starts clean.  `workspace` is int32, zero on
-// entry and left zero.
+// SiLU-packed down GEMM), as one call, bit-identical to the two ops (two
+// launches, the gate_up one storing fp16(silu(g) * u) where its tiles pair the
+// gate and up chunks).  `workspace` is int32, zero on entry and left zero.
 void lowbit_marlin_mlp_fused_out(torch::Tensor gate_up_qweight, torch::Tensor gate_up_scales,
                                  torch::Tensor down_qweight, torch::Tensor down_scales, torch::Tensor x,
                                  torch::Tensor out, torch::Tensor workspace, int64_t hidden, int64_t intermediate,
-                                 int64_t gate_group_size, int64_t down_group_size, int64_t mode, bool check) {
+                                 int64_t gate_group_size, int64_t down_group_size) {
   LB_CHECK_DEV(gate_up_qweight); LB_CHECK_DEV(gate_up_scales); LB_CHECK_DEV(down_qweight); LB_CHECK_DEV(down_scales);
   LB_CHECK_DEV(x); LB_CHECK_DEV(out); LB_CHECK_DEV(workspace);
   LB_CHECK_CONTIG(gate_up_qweight); LB_CHECK_CONTIG(gate_up_scales); LB_CHECK_CONTIG(down_qweight);
@@ -352,19 +392,12 @@ void lowbit_marlin_mlp_fused_out(torch::Tensor gate_up_qweight, torch::Tensor ga
   const int64_t ws_need = lb_marlin_mlp_fused_workspace_len(batch, hidden, intermediate);
   TORCH_CHECK(workspace.numel() >= ws_need, "workspace must hold at least ", ws_need, " int32 elements");
   const c10::DeviceGuard guard(x.device());
-  const size_t bytes = lb_marlin_mlp_fused_scratch_bytes(batch, hidden, intermediate);
-  auto scratch = torch::empty({(int64_t)std::max<size_t>(bytes, 1)}, x.options().dtype(torch::kUInt8));
+  auto scratch = op_scratch(lb_marlin_mlp_fused_scratch_bytes(batch, hidden, intermediate), x);
   lb_ok(lb_marlin_mlp_fused(h16(x), gate_up_qweight.data_ptr<int32_t>(), h16(gate_up_scales),
                             down_qweight.data_ptr<int32_t>(), h16(down_scales), h16m(out), batch, hidden,
-                            intermediate, gate_group, down_group, (int32_t)mode, workspace.data_ptr<int32_t>(),
-                            workspace.numel(), scratch.data_ptr(), (size_t)scratch.numel(), stream_of(x)),
+                            intermediate, gate_group, down_group, workspace.data_ptr<int32_t>(), workspace.numel(),
+                            scratch.ptr, scratch.bytes, stream_of(x)),
         "lowbit_marlin_mlp_fused_out");
-  if (check) {
-    const int st = lb_marlin_mlp_fused_check(workspace.data_ptr<int32_t>(), workspace.numel(), stream_of(x));
-    TORCH_CHECK(st != LB_ERR_HANDOFF, "lowbit_marlin_mlp_fused_out: the one-launch hand-off gave up waiting; the "
-                "output of this call is not valid (workspace zeroed)");
-    lb_ok(st, "lowbit_marlin_mlp_fused_out check");
-  }
 }
 
 // Dense fp16 W[N, K] of a Marlin tensor (no reference op; the reference's
@@ -426,10 +459,11 @@ PYBIND11_MODULE(langburst_cuda, m) {
   m.def("lowbit_marlin_dequant", &lowbit_marlin_dequant, "Dense fp16 W[N, K] of a Marlin tensor",
         py::arg("qweight"), py::arg("scales"), py::arg("cols"), py::arg("group_size"));
   m.def("lowbit_marlin_mlp_fused_out", &lowbit_marlin_mlp_fused_out,
-        "Marlin W4A16 decode MLP: down(SiLU(gate) * up) of x; mode 1 asks for one launch, check=True verifies it",
+        "Marlin W4A16 decode MLP: down(SiLU(gate) * up) of x, bit-identical to the gate_up GEMM then the "
+        "SiLU-packed down GEMM",
         py::arg("gate_up_qweight"), py::arg("gate_up_scales"), py::arg("down_qweight"), py::arg("down_scales"),
         py::arg("x"), py::arg("out"), py::arg("workspace"), py::arg("hidden"), py::arg("intermediate"),
-        py::arg("gate_group_size"), py::arg("down_group_size"), py::arg("mode") = 0, py::arg("check") = false);
+        py::arg("gate_group_size"), py::arg("down_group_size"));
   m.def("lowbit_marlin_mlp_fused_workspace_len",
         [](int64_t batch, int64_t hidden, int64_t intermediate) {
           return lb_marlin_mlp_fused_workspace_len(batch, hidden, intermediate);

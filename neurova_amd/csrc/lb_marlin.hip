@@ -1,13 +1,11 @@
 // Host dispatch and C-ABI entry points for the Marlin-layout W4A16 path:
 // GEMM (decode and prefill kernels), SiLU-gated A prologue, fused argmax,
-// dense dequant, the streaming MLP and the one-launch decode MLP.
+// dense dequant, the streaming MLP and the two-launch decode MLP.
 
 #include <stdlib.h>
 
 #include <algorithm>
 
-#include <atomic>
-#include <mutex>
 
 #include "marlin_gemm.hpp"
 #include "marlin_run.hpp"
@@ -286,8 +284,8 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 }
 
 // `am`: the A mode of the launch (gemm::A_PLAIN or gemm::A_SILU_PACKED);
-// `argmax`: the fused-argmax variant; `allow_direct`: false plans only the
-// staged decode tiles (the one-launch MLP's phases).
+// `argmax`: the fused-argmax variant; `allow_mixed`: the mixed whole-K plan
+// may be used (grouped scales only).
 //
 // Which decode form (measured on the decode shapes of BASELINE.json): the direct
 // form where the tiles are narrow (the waves of a workgroup then share
@@ -298,15 +296,11 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // form first forms fp16(silu(g) * u) in a launch of its own, which does not
 // pay below 5 rows.  M = 17..32: the direct form on 64-column tiles, the
 // ring on 4-chunk tiles; 2-chunk tiles go to the prefill kernel.
-#ifndef LB_MIXED_MAX_PER_CU
-#define LB_MIXED_MAX_PER_CU 2
-#endif
-#ifndef LB_MIXED_MAX_M
-#define LB_MIXED_MAX_M 4
-#endif
+constexpr int64_t kMixedMaxPerCu = 2;  // whole-K tiles per CU (more was not measured)
+constexpr int64_t kMixedMaxM = 4;      // rows (measured at M = 1..4)
 
 inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am, bool argmax = false,
-                      bool allow_direct = true, bool allow_mixed = true) {
+                      bool allow_mixed = true) {
   Plan pl;
   pl.n_cg = (int)(n / 256);
   const int groups = (int)(k / 128);
@@ -327,12 +321,12 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
   // Two whole-K tiles per CU where the chunks number two to 2 1/8 per CU
   // (gate/up, N = 34816: 21.2 against 21.9 us; N = 33280: 19.6 against 21.4;
   // K = 4096, N = 32768: 15.5 against 16.8 us); more per CU is not measured.
-  if (m <= LB_MIXED_MAX_M && allow_direct && allow_mixed && !argmax && am == gemm::A_PLAIN) {
+  if (m <= kMixedMaxM && allow_mixed && !argmax && am == gemm::A_PLAIN) {
     const int64_t chunks = n / 64, cus = device_cus();
     const int ksub = skinny::kWaves;  // 1-chunk tiles: the four waves share the k range
     // (measured at K <= 5120 and up to CUs / 8 leftover chunks; a longer K or
     // more leftover work per CU keeps the split tiles)
-    const int64_t per = std::min<int64_t>(chunks / cus, LB_MIXED_MAX_PER_CU), whole = per * cus;
+    const int64_t per = std::min<int64_t>(chunks / cus, kMixedMaxPerCu), whole = per * cus;
     if (per >= 1 && (chunks - whole) * 8 <= cus && groups >= ksub && k <= 5120) {
       const int64_t left = chunks - whole;
       const int s = left > 0 ? (int)std::min<int64_t>(std::min<int64_t>(cus / left, groups / ksub), m >= 4 ? 6 : 256) : 1;
@@ -353,7 +347,7 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
     }
   }
   const Tiling ts = m <= skinny::kMaxM ? staged_tiling(m, n, k, workspace_len) : Tiling{};
-  const Tiling td = (allow_direct && !argmax && m <= 16 * skinny::kMaxMR) ? direct_tiling(m, n, k, workspace_len)
+  const Tiling td = (!argmax && m <= 16 * skinny::kMaxMR) ? direct_tiling(m, n, k, workspace_len)
                                                                          : Tiling{};
   bool direct = false;
   if (td.cpw > 0) {
@@ -461,7 +455,7 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   if (k * n / 2 >= (1LL << 32)) return LB_ERR_PROB_SHAPE;
   const bool gated = var == V_SILU || var == V_SILU_DONE;
   const Plan pl = make_plan(m, n, k, workspace_len, gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, var == V_ARGMAX,
-                            true, grouped != 0);
+                            grouped != 0);
   if (var == V_SILU_DONE && !pl.skinny) return LB_ERR_ARG;  // decode batches only
   if (workspace_len < counters_needed(pl, var == V_ARGMAX)) return LB_ERR_WORKSPACE;
   const size_t need = pl.partial_bytes + (var == V_ARGMAX ? pl.keys_bytes : 0) + (var == V_SILU ? pl.act_bytes : 0);
@@ -586,7 +580,6 @@ extern "C" const char* lb_status_string(int status) {
     case LB_ERR_WORKSPACE: return "workspace too small";
     case LB_ERR_SCRATCH: return "scratch too small";
     case LB_ERR_HIP: return "HIP runtime error";
-    case LB_ERR_HANDOFF: return "in-kernel hand-off gave up; output not valid";
     case LB_ERR_NOALLOC_LIMIT: return "problem needs more than the static no-allocation scratch";
     default: return "unknown status";
   }
@@ -601,7 +594,7 @@ extern "C" size_t lb_marlin_scratch_bytes(int64_t prob_m, int64_t prob_n, int64_
   // Largest over the variants (the SiLU-gated one may use other tiles).
   // (with and without the mixed plan, which only grouped scales take)
   const marlin::Plan a = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN);
-  const marlin::Plan a2 = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN, false, true, false);
+  const marlin::Plan a2 = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN, false, false);
   const marlin::Plan b = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_SILU_PACKED);
   const marlin::Plan c = marlin::make_plan(prob_m, prob_n, prob_k, INT64_MAX, gemm::A_PLAIN, true);
   return std::max(std::max(std::max(a.partial_bytes + a.keys_bytes, a2.partial_bytes + a2.keys_bytes),
@@ -619,7 +612,7 @@ extern "C" int lb_marlin_describe_plan(int64_t prob_m, int64_t prob_n, int64_t p
   if (prob_m == 0 || prob_n == 0 || prob_k == 0) return LB_OK;
   const bool argmax = variant == 2, gated = variant == 1;
   const marlin::Plan pl = marlin::make_plan(prob_m, prob_n, prob_k, workspace_len,
-                                            gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, argmax, true, grouped != 0);
+                                            gated ? gemm::A_SILU_PACKED : gemm::A_PLAIN, argmax, grouped != 0);
   if (pl.skinny) {
     out[0] = !pl.direct ? 0 : pl.cpw == skinny::kWaves ? 2 : 1;
     out[1] = pl.cpw;
@@ -750,128 +743,35 @@ extern "C" int lb_marlin_mlp_streaming(const int32_t* gate_up_qweight, const uin
 }
 
 // ---------------------------------------------------------------------------
-// Decode MLP in one launch (marlin_mlp.hpp)
+// Decode MLP: gate_up, then down over fp16(silu(g) * u) (marlin_mlp.hpp)
 // ---------------------------------------------------------------------------
 namespace {
 struct FusedMlpPlan {
-  marlin::Plan up, down;  // the one launch's staged tilings
-  marlin::Plan up2, down2;  // the tilings the two projections plan as separate calls
-  bool one_launch = false;
-  bool act_path = false;  // two launches: gate_up stores fp16(silu(g) * u), no [g | u] round trip
-  int wgs = 0;
-  size_t lds = 0;
-  size_t up_partial = 0, act = 0, down_partial = 0;  // scratch offsets
-  size_t mixed = 0;                                  // two-launch form: [g | u] fp16
-  size_t scratch = 0;      // bytes this launch uses
-  size_t scratch_max = 0;  // bytes either form uses
-  int64_t ws_up = 0, ws_down = 0, ws_len = 0;        // workspace offsets, length
+  marlin::Plan up, down;  // the tilings lb_marlin_gemm plans for the two projections
+  bool act_path = false;  // gate_up stores fp16(silu(g) * u), no [g | u] round trip
+  size_t partial = 0;     // scratch: [g | u] or the activations first, then either launch's own scratch
+  size_t scratch = 0;
+  int64_t ws_down = 0, ws_len = 0;  // workspace: the gate_up launch's counters, then the down launch's
 };
 
-using FusedKernel = void (*)(mlp::FusedParams);
-
-template <bool G1, bool G2>
-FusedKernel fused_kernel_g(int cpw1, int cpw2) {
-  if (cpw1 == 4) {
-    if (cpw2 == 4) return mlp::marlin_mlp_fused_kernel<G1, 4, G2, 4>;
-    if (cpw2 == 2) return mlp::marlin_mlp_fused_kernel<G1, 4, G2, 2>;
-    return mlp::marlin_mlp_fused_kernel<G1, 4, G2, 1>;
-  }
-  if (cpw2 == 4) return mlp::marlin_mlp_fused_kernel<G1, 2, G2, 4>;
-  if (cpw2 == 2) return mlp::marlin_mlp_fused_kernel<G1, 2, G2, 2>;
-  return mlp::marlin_mlp_fused_kernel<G1, 2, G2, 1>;
+// Counters a launch of `pl` may use (planned with an unbounded workspace).
+int64_t fused_counters(const marlin::Plan& pl) {
+  return std::max<int64_t>(1 + std::max<int64_t>(pl.n_cg, pl.tail_tiles), marlin::counters_needed(pl, false));
 }
 
-FusedKernel fused_kernel(bool g1, bool g2, int cpw1, int cpw2) {
-  if (g1) return g2 ? fused_kernel_g<true, true>(cpw1, cpw2) : fused_kernel_g<true, false>(cpw1, cpw2);
-  return g2 ? fused_kernel_g<false, true>(cpw1, cpw2) : fused_kernel_g<false, false>(cpw1, cpw2);
-}
-
-// Workgroups of `fn` resident per CU with `lds` bytes of dynamic LDS, cached.
-int resident_per_cu(FusedKernel fn, size_t lds) {
-  struct Entry { FusedKernel fn; size_t lds; int dev; int v; };
-  static std::mutex mu;
-  static Entry cache[64];
-  static int used = 0;
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess) return 0;
-  std::lock_guard<std::mutex> lock(mu);
-  for (int i = 0; i < used; ++i)
-    if (cache[i].fn == fn && cache[i].lds == lds && cache[i].dev == dev) return cache[i].v;
-  int v = 0;
-  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, reinterpret_cast<const void*>(fn), skinny::kThreads, lds) !=
-      hipSuccess)
-    v = 0;
-  if (used < 64) cache[used++] = Entry{fn, lds, dev, v};
-  return v;
-}
-
-// Launch modes of lb_marlin_mlp_fused.  Auto takes the two launches: the one
-// launch (faster from batch 4 on, where its down phase stages plain
-// activations instead of SiLU-gating [g | u]) relies on bounded in-kernel
-// waits, so it runs only when the caller asks for it (mode 1).
-enum { kMlpAuto = 0, kMlpOne = 1, kMlpTwo = 2 };
-
-std::atomic<int> g_mlp_spin_limit{mlp::kSpinLimit};
-
-// occupancy == false: plan the layouts only (no device query; two launches).
-FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g1, bool g2, int mode,
-                            bool occupancy = true) {
+FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g1, bool g2) {
   FusedMlpPlan p;
-  // the one launch runs the staged decode tiles; the two launches plan as lb_marlin_gemm does
-  p.up = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN, false, false);
-  p.down = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED, false, false);
-  const marlin::Plan up2 = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN);
-  const marlin::Plan down2 = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED);
-  p.up2 = up2;
-  p.down2 = down2;
-  // decode tiles of 2 or 4 chunks pair gate and up chunks; 64-column tiles
-  // (direct A at M = 17..32) and prefill tiles take the [g | u] round trip
-  p.act_path = up2.skinny && up2.cpw >= 2 && down2.skinny;
-  const bool wanted = mode == kMlpOne;
-  // The one launch must sum every output as the two launches do (bit-identical
-  // results): only where both projections plan the same staged tiles.
-  auto same = [](const marlin::Plan& a, const marlin::Plan& b) {
-    return a.skinny && b.skinny && !b.direct && a.cpw == b.cpw && a.splits == b.splits;
-  };
-  if (p.up.skinny && p.up.cpw >= 2 && p.down.skinny && p.down.splits <= mlp::kMaxSplits && same(p.up, up2) &&
-      same(p.down, down2)) {
-    p.wgs = std::max(p.up.n_cg * p.up.splits, p.down.n_cg * p.down.splits);
-    p.lds = std::max(p.up.lds, p.down.lds);
-    if (occupancy && wanted) {
-      const int per_cu = resident_per_cu(fused_kernel(g1, g2, p.up.cpw, p.down.cpw), p.lds);
-      p.one_launch = (int64_t)p.wgs <= (int64_t)per_cu * marlin::device_cus();
-    }
-  }
-  // one launch: gate_up partials | activations [batch][inter] fp16 | down partials
-  const size_t up_off = 0;
-  const size_t act_off = up_off + p.up.partial_bytes;
-  const size_t down_off = act_off + marlin::align_up((size_t)batch * (size_t)inter * 2);
-  const size_t one_bytes = down_off + p.down.partial_bytes;
-  // two launches: [g | u] fp16, then either projection's own scratch
-  const size_t after = marlin::align_up((size_t)batch * (size_t)(2 * inter) * 2);
-  const size_t two_bytes = after + std::max(lb_marlin_scratch_bytes(batch, 2 * inter, hidden, 128),
-                                            lb_marlin_scratch_bytes(batch, hidden, inter, 128));
-  p.scratch_max = std::max(one_bytes, two_bytes);
-  if (p.one_launch) {
-    p.up_partial = up_off;
-    p.act = act_off;
-    p.down_partial = down_off;
-    p.scratch = one_bytes;
-  } else {
-    p.mixed = 0;
-    p.up_partial = p.down_partial = after;
-    p.scratch = two_bytes;
-  }
-  // workspace: the hand-off counters and fault flag, then each projection's counters
-  p.ws_up = mlp::kSyncWorkspace;
-  p.ws_down = p.ws_up + std::max(std::max<int64_t>(1 + std::max<int64_t>(p.up.n_cg, p.up.tail_tiles),
-                                                    marlin::counters_needed(p.up, false)),
-                                  std::max<int64_t>(1 + std::max<int64_t>(up2.n_cg, up2.tail_tiles),
-                                                    marlin::counters_needed(up2, false)));
-  p.ws_len = p.ws_down + std::max(std::max<int64_t>(1 + std::max<int64_t>(p.down.n_cg, p.down.tail_tiles),
-                                                    marlin::counters_needed(p.down, false)),
-                                  std::max<int64_t>(1 + std::max<int64_t>(down2.n_cg, down2.tail_tiles),
-                                                    marlin::counters_needed(down2, false)));
+  // as run() plans each projection (the mixed decode plan only with grouped scales)
+  p.up = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN, false, g1);
+  p.down = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED, false, g2);
+  // decode tiles of 2 or 4 chunks pair gate and up chunks; single-chunk tiles
+  // and prefill tiles take the [g | u] round trip
+  p.act_path = p.up.skinny && p.up.cpw >= 2 && p.down.skinny;
+  p.partial = marlin::align_up((size_t)batch * (size_t)(2 * inter) * 2);
+  p.scratch = p.partial + std::max(lb_marlin_scratch_bytes(batch, 2 * inter, hidden, g1 ? 128 : -1),
+                                   lb_marlin_scratch_bytes(batch, hidden, inter, g2 ? 128 : -1));
+  p.ws_down = fused_counters(p.up);
+  p.ws_len = p.ws_down + fused_counters(p.down);
   return p;
 }
 
@@ -886,61 +786,54 @@ int fused_mlp_check(int64_t batch, int64_t hidden, int64_t inter, int64_t gate_g
 }
 }  // namespace
 
+// Sizes cover grouped and per-column scales alike.
 extern "C" size_t lb_marlin_mlp_fused_scratch_bytes(int64_t batch, int64_t hidden, int64_t intermediate) {
   int g1 = 0, g2 = 0;
   if (batch <= 0 || fused_mlp_check(batch, hidden, intermediate, 128, 128, g1, g2) != LB_OK) return 0;
-  return fused_mlp_plan(batch, hidden, intermediate, true, true, kMlpTwo, false).scratch_max;
+  return std::max(fused_mlp_plan(batch, hidden, intermediate, true, true).scratch,
+                  fused_mlp_plan(batch, hidden, intermediate, false, false).scratch);
 }
 
 extern "C" int64_t lb_marlin_mlp_fused_workspace_len(int64_t batch, int64_t hidden, int64_t intermediate) {
   int g1 = 0, g2 = 0;
   if (batch <= 0 || fused_mlp_check(batch, hidden, intermediate, 128, 128, g1, g2) != LB_OK) return 0;
-  return fused_mlp_plan(batch, hidden, intermediate, true, true, kMlpTwo, false).ws_len;
-}
-
-extern "C" int lb_marlin_mlp_fused_launches(int64_t batch, int64_t hidden, int64_t intermediate,
-                                            int64_t gate_group_size, int64_t down_group_size, int32_t mode) {
-  int g1 = 0, g2 = 0;
-  const int st = fused_mlp_check(batch, hidden, intermediate, gate_group_size, down_group_size, g1, g2);
-  if (st != LB_OK) return -st;
-  if (mode < kMlpAuto || mode > kMlpTwo) return -LB_ERR_ARG;
-  if (batch == 0) return 0;
-  return fused_mlp_plan(batch, hidden, intermediate, g1, g2, mode).one_launch ? 1 : 2;
+  return std::max(fused_mlp_plan(batch, hidden, intermediate, true, true).ws_len,
+                  fused_mlp_plan(batch, hidden, intermediate, false, false).ws_len);
 }
 
 extern "C" int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qweight, const uint16_t* gate_up_scales,
                                    const int32_t* down_qweight, const uint16_t* down_scales, uint16_t* out,
                                    int64_t batch, int64_t hidden, int64_t intermediate, int64_t gate_group_size,
-                                   int64_t down_group_size, int32_t mode, int32_t* workspace, int64_t workspace_len,
+                                   int64_t down_group_size, int32_t* workspace, int64_t workspace_len,
                                    void* scratch, size_t scratch_bytes, lb_stream_t stream) {
   int g1 = 0, g2 = 0;
   const int st0 = fused_mlp_check(batch, hidden, intermediate, gate_group_size, down_group_size, g1, g2);
   if (st0 != LB_OK) return st0;
-  if (mode < kMlpAuto || mode > kMlpTwo) return LB_ERR_ARG;
   if (batch == 0) return LB_OK;
   if (!x || !gate_up_qweight || !gate_up_scales || !down_qweight || !down_scales || !out || !workspace)
     return LB_ERR_ARG;
   if (!lbh::aligned(x, 16) || !lbh::aligned(gate_up_qweight, 16) || !lbh::aligned(gate_up_scales, 16) ||
       !lbh::aligned(down_qweight, 16) || !lbh::aligned(down_scales, 16) || !lbh::aligned(out, 2))
     return LB_ERR_ALIGN;
-  const FusedMlpPlan pl = fused_mlp_plan(batch, hidden, intermediate, g1, g2, mode);
+  const FusedMlpPlan pl = fused_mlp_plan(batch, hidden, intermediate, g1 != 0, g2 != 0);
   if (workspace_len < pl.ws_len) return LB_ERR_WORKSPACE;
   if (!scratch || scratch_bytes < pl.scratch) return LB_ERR_SCRATCH;
   if (!lbh::aligned(scratch, 256)) return LB_ERR_ALIGN;
   unsigned char* sc = reinterpret_cast<unsigned char*>(scratch);
   hipStream_t st = (hipStream_t)stream;
   const int64_t n_up = 2 * intermediate;
+  const size_t rest = scratch_bytes - pl.partial;
 
-  if (!pl.one_launch && pl.act_path) {
-    // gate_up -> fp16(silu(g) * u) [batch][intermediate] (in the [g | u]
-    // region), then the down projection over it with the SiLU-gated op's own
+  if (pl.act_path) {
+    // gate_up -> fp16(silu(g) * u) [batch][intermediate] (at the start of
+    // scratch), then the down projection over it with the SiLU-gated op's own
     // plan: the same sums as the two reference calls
-    uint16_t* act = reinterpret_cast<uint16_t*>(sc + pl.mixed);
-    const marlin::Plan& u2 = pl.up2;
+    uint16_t* act = reinterpret_cast<uint16_t*>(sc);
+    const marlin::Plan& u2 = pl.up;
     skinny::Params u{};
     u.a = x; u.b = reinterpret_cast<const uint32_t*>(gate_up_qweight); u.s = gate_up_scales; u.c = nullptr;
-    u.counters = workspace + pl.ws_up;
-    u.partial = u2.partial_bytes ? reinterpret_cast<float*>(sc + pl.up_partial) : nullptr;
+    u.counters = workspace;
+    u.partial = u2.partial_bytes ? reinterpret_cast<float*>(sc + pl.partial) : nullptr;
     u.m = (int)batch; u.n = (int)n_up; u.k = (int)hidden; u.splits = u2.splits;
     u.kp_total = (int)(hidden / 32); u.n_cg = u2.n_cg;
     u.act_out = reinterpret_cast<uint32_t*>(act);
@@ -968,62 +861,16 @@ extern "C" int lb_marlin_mlp_fused(const uint16_t* x, const int32_t* gate_up_qwe
 #undef LB_ACT
     const int e = lbh::launch_status();
     if (e != LB_OK) return e;
-    const size_t rest = scratch_bytes - pl.down_partial;
     return marlin::run(marlin::V_SILU_DONE, act, down_qweight, out, down_scales, batch, hidden, intermediate,
                        workspace + pl.ws_down, workspace_len - pl.ws_down, down_group_size, nullptr, nullptr,
-                       sc + pl.down_partial, rest, st);
+                       sc + pl.partial, rest, st);
   }
 
-  if (!pl.one_launch) {
-    uint16_t* mixed = reinterpret_cast<uint16_t*>(sc + pl.mixed);
-    const size_t rest = scratch_bytes - pl.up_partial;
-    int e = marlin::run(marlin::V_PLAIN, x, gate_up_qweight, mixed, gate_up_scales, batch, n_up, hidden,
-                        workspace + pl.ws_up, workspace_len - pl.ws_up, gate_group_size, nullptr, nullptr,
-                        sc + pl.up_partial, rest, st);
-    if (e != LB_OK) return e;
-    return marlin::run(marlin::V_SILU, mixed, down_qweight, out, down_scales, batch, hidden, intermediate,
-                       workspace + pl.ws_down, workspace_len - pl.ws_down, down_group_size, nullptr, nullptr,
-                       sc + pl.down_partial, rest, st);
-  }
-
-  mlp::FusedParams f{};
-  skinny::Params& u = f.up;
-  u.a = x; u.b = reinterpret_cast<const uint32_t*>(gate_up_qweight); u.s = gate_up_scales; u.c = nullptr;
-  u.counters = workspace + pl.ws_up;
-  u.partial = pl.up.partial_bytes ? reinterpret_cast<float*>(sc + pl.up_partial) : nullptr;
-  u.m = (int)batch; u.n = (int)n_up; u.k = (int)hidden; u.splits = pl.up.splits;
-  u.kp_total = (int)(hidden / 32); u.n_cg = pl.up.n_cg;
-  u.act_out = reinterpret_cast<uint32_t*>(sc + pl.act);
-  u.gate_chunks = (int)(intermediate / 64);
-  skinny::Params& d = f.down;
-  d.a = reinterpret_cast<const uint16_t*>(sc + pl.act);
-  d.b = reinterpret_cast<const uint32_t*>(down_qweight); d.s = down_scales; d.c = out;
-  d.counters = workspace + pl.ws_down;
-  d.partial = pl.down.partial_bytes ? reinterpret_cast<float*>(sc + pl.down_partial) : nullptr;
-  d.m = (int)batch; d.n = (int)hidden; d.k = (int)intermediate; d.splits = pl.down.splits;
-  d.kp_total = (int)(intermediate / 32); d.n_cg = pl.down.n_cg;
-  f.ws = workspace;
-  f.spin_limit = g_mlp_spin_limit.load(std::memory_order_relaxed);
-  hipLaunchKernelGGL(fused_kernel(g1, g2, pl.up.cpw, pl.down.cpw), dim3((unsigned)pl.wgs), dim3(skinny::kThreads),
-                     pl.lds, st, f);
-  return lbh::launch_status();
-}
-
-extern "C" int lb_marlin_mlp_fused_check(int32_t* workspace, int64_t workspace_len, lb_stream_t stream) {
-  if (!workspace || workspace_len < 2) return LB_ERR_ARG;
-  hipStream_t st = (hipStream_t)stream;
-  int32_t flag = 0;
-  if (hipStreamSynchronize(st) != hipSuccess) return LB_ERR_HIP;
-  if (hipMemcpy(&flag, workspace + 1, sizeof(flag), hipMemcpyDeviceToHost) != hipSuccess) return LB_ERR_HIP;
-  if (flag == 0) return LB_OK;
-  // a late producer may have counted a tile after its split's counters were
-  // reset: clear every entry, then report the call
-  if (hipMemsetAsync(workspace, 0, (size_t)workspace_len * sizeof(int32_t), st) != hipSuccess ||
-      hipStreamSynchronize(st) != hipSuccess)
-    return LB_ERR_HIP;
-  return LB_ERR_HANDOFF;
-}
-
-extern "C" void lb_marlin_mlp_fused_set_spin_limit(int32_t polls) {
-  g_mlp_spin_limit.store(polls >= 1 ? polls : mlp::kSpinLimit, std::memory_order_relaxed);
+  uint16_t* mixed = reinterpret_cast<uint16_t*>(sc);
+  int e = marlin::run(marlin::V_PLAIN, x, gate_up_qweight, mixed, gate_up_scales, batch, n_up, hidden, workspace,
+                      pl.ws_down, gate_group_size, nullptr, nullptr, sc + pl.partial, rest, st);
+  if (e != LB_OK) return e;
+  return marlin::run(marlin::V_SILU, mixed, down_qweight, out, down_scales, batch, hidden, intermediate,
+                     workspace + pl.ws_down, workspace_len - pl.ws_down, down_group_size, nullptr, nullptr,
+                     sc + pl.partial, rest, st);
 }

@@ -64,12 +64,10 @@ constexpr int kSteps = 4;               // 32-k steps per batch (one scale group
 constexpr int kStageUnroll = 8;         // A staging: 16-byte items in flight per thread
 constexpr int kDepth = 2;               // weight batches in flight
 
-// A_HANDOFF: plain fp16 A written earlier in the same launch by other
-// workgroups (the fused MLP's activations), read with device-coherent loads.
 // A_DIRECT: plain fp16 A, not staged: fragments loaded per step (M up to 32).
 // A_RING: plain fp16 A staged one batch (one scale group) at a time through a
 // two-slot LDS ring, for 4-chunk tiles whose waves share it (M up to 32).
-enum AMode { A_PLAIN = 0, A_SILU_PACKED = 1, A_HANDOFF = 2, A_DIRECT = 3, A_RING = 4 };
+enum AMode { A_PLAIN = 0, A_SILU_PACKED = 1, A_DIRECT = 3, A_RING = 4 };
 // EPI_ACT: the tile pairs gate and up chunks (gate_up projection of an MLP)
 // and stores fp16(silu(g) * u) of its fp16 outputs instead of the outputs.
 enum EpiMode { EPI_STORE = 0, EPI_ARGMAX = 1, EPI_ACT = 2 };
@@ -294,20 +292,14 @@ __device__ __forceinline__ bool wave_epilogue(const Params& p, const f32x4 (&acc
   return true;
 }
 
-struct NoWait {
-  __device__ void operator()() const {}
-};
-
 // One workgroup's share of the projection: column tile cg (64 * CPW columns),
 // k split `split`.  CPW: chunks per workgroup (4, 2 or 1), a compile-time
 // constant so that the wide-N instantiation (CPW = 4) carries no k-share
-// arithmetic.  Uses the kernel's dynamic LDS.  A_HANDOFF: the first weight
-// batches are fetched, then `wait_for_a()` (every thread calls it) waits
-// until A has been written, then A is staged.  Returns true in the workgroup
+// arithmetic.  Uses the kernel's dynamic LDS.  Returns true in the workgroup
 // that stored the tile's outputs (EPI_STORE, EPI_ACT) or ran the launch's
 // final argmax reduction.
-template <int AM, int EPI, bool GROUPED, int CPW, int MR = 1, typename WaitA = NoWait>
-__device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const int split, WaitA wait_for_a = WaitA()) {
+template <int AM, int EPI, bool GROUPED, int CPW, int MR = 1>
+__device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const int split) {
   static_assert(EPI != EPI_ACT || CPW >= 2, "EPI_ACT pairs a gate and an up chunk");
   static_assert(MR == 1 || ((AM == A_DIRECT || AM == A_RING) && (EPI == EPI_STORE || EPI == EPI_ACT)),
                 "row blocks > 1: direct or ring A, store or SiLU-gated epilogue");
@@ -320,9 +312,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   __shared__ int s_prev;
   __shared__ uint64_t s_keys[kWaves][kMaxM];
   // Every kernel argument the prologue needs, named before any other work
-  // (those of marlin_skinny_kernel are preloaded; through a struct, as in
-  // the one-launch MLP, they are fetched in one round trip instead of two
-  // dependent ones: the split fields, a division, then the pointers).
+  // (the kernels pass them as scalar arguments, preloaded into SGPRs).
   asm volatile("" ::"s"(p.a), "s"(p.b), "s"(p.s), "s"(p.m), "s"(p.n), "s"(p.k), "s"(p.splits), "s"(p.kp_total));
   const int tid = threadIdx.x;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);  // uniform: the ring's offsets stay scalar
@@ -384,7 +374,6 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   // never reaches the next integer); octs >= 16.
   const uint32_t oct_magic = 0xffffffffu / (uint32_t)octs + 1u;
   const int64_t a_row_stride = AM == A_SILU_PACKED ? 2 * (int64_t)p.k : (int64_t)p.k;
-  const __amdgpu_buffer_rsrc_t ra = buffer_of(p.a, (uint32_t)((int64_t)mrows * p.k * 2));  // A_HANDOFF
   uint4 gv[kStageUnroll], uv[kStageUnroll];
   auto stage_load = [&](int base) __attribute__((always_inline)) {
 #pragma unroll
@@ -393,10 +382,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
       const int mm = (int)__umulhi((uint32_t)it, oct_magic);
       const int r = it - mm * octs;
       const uint16_t* src = p.a + (int64_t)mm * a_row_stride + k0 + (r << 3);
-      if (AM == A_HANDOFF)
-        gv[u] = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(ra, (uint32_t)(src - p.a) * 2u, 0, kSc1));
-      else
-        gv[u] = *reinterpret_cast<const uint4*>(src);
+      gv[u] = *reinterpret_cast<const uint4*>(src);
       if (AM == A_SILU_PACKED) uv[u] = *reinterpret_cast<const uint4*>(src + p.k);
     }
   };
@@ -491,9 +477,9 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   };
 
   // ---- staging loads, then the first weight batches, then the stores ----
-  // (A_HANDOFF: the weight batches first, then the wait for A; A_DIRECT: no
-  // staging; A_RING: batch 0 of A, then per weight batch i the A batch i + 1)
-  if (AM != A_HANDOFF && !kDirect && !kRing) stage_load(0);
+  // (A_DIRECT: no staging; A_RING: batch 0 of A, then per weight batch i the
+  // A batch i + 1)
+  if (!kDirect && !kRing) stage_load(0);
   if constexpr (kRing) ring_load(ar0, 0);
   __builtin_amdgcn_sched_barrier(0);  // staging loads strictly before the weight loads
 #pragma unroll
@@ -501,10 +487,6 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     issue(i, min(i, nb - 1));
     if constexpr (kRing) ring_load(ar[i], min(i + 1, nb - 1));
     __builtin_amdgcn_sched_barrier(0);  // keep slot order: the loop's waits assume it
-  }
-  if (AM == A_HANDOFF) {
-    wait_for_a();
-    stage_load(0);
   }
   if constexpr (kRing) {
     __builtin_amdgcn_sched_barrier(0);

@@ -231,11 +231,14 @@ class LowBitMarlinTensor:
         if have is not None and have.device == dev and tuple(have.shape) == shape and have.dtype == dtype:
             return have
         nbytes = int(np.prod(shape)) * torch.empty((), dtype=dtype).element_size()
-        out = torch.empty(shape, device=dev, dtype=dtype)
+        # admission is decided before the allocation, so that the free-memory
+        # check sees the device as it is (loader.py:254-264)
         if _OutputCache.admits(batch, dev, nbytes):
+            out = torch.empty(shape, device=dev, dtype=dtype)
             _OutputCache.account(nbytes - _nbytes(have))
             cache[batch] = out
-        return out
+            return out
+        return torch.empty(shape, device=dev, dtype=dtype)
 
     def _cached_workspace(self):
         import torch
@@ -246,11 +249,12 @@ class LowBitMarlinTensor:
         if ws is not None and ws.device == dev and ws.numel() >= size:
             ws[:size].zero_()
             return ws
-        fresh = torch.zeros((size,), device=dev, dtype=torch.int32)
-        if _OutputCache.admits(1, dev, size * 4):
+        if _OutputCache.admits(1, dev, size * 4):  # before the allocation (loader.py:290-302)
+            fresh = torch.zeros((size,), device=dev, dtype=torch.int32)
             _OutputCache.account(size * 4 - _nbytes(ws))
             self._workspace = fresh
-        return fresh
+            return fresh
+        return torch.zeros((size,), device=dev, dtype=torch.int32)
 
     def runtime_cache_bytes(self) -> int:
         total = _nbytes(self._workspace) + _nbytes(self._argmax_sync)

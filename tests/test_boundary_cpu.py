@@ -98,33 +98,25 @@ def test_scratch_sizes(L):
 
 
 def _mlp_fused(L, batch=1, hidden=5120, inter=17408, gg=128, dg=128, x=FAKE, out=FAKE, ws_len=None, scratch=FAKE,
-               scratch_bytes=None, mode=0):
+               scratch_bytes=None):
     ws_len = L.lb_marlin_mlp_fused_workspace_len(1, hidden, inter) if ws_len is None else ws_len
     sb = L.lb_marlin_mlp_fused_scratch_bytes(1, hidden, inter) if scratch_bytes is None else scratch_bytes
-    return L.lb_marlin_mlp_fused(x, FAKE, FAKE, FAKE, FAKE, out, batch, hidden, inter, gg, dg, mode, FAKE, ws_len,
+    return L.lb_marlin_mlp_fused(x, FAKE, FAKE, FAKE, FAKE, out, batch, hidden, inter, gg, dg, FAKE, ws_len,
                                  scratch, sb, None)
 
 
 def test_mlp_fused_rejection_and_sizes(L):
     h, i = 5120, 17408
-    launches = lambda b, hh=h, ii=i, gg=128, dg=128, mode=0: L.lb_marlin_mlp_fused_launches(b, hh, ii, gg, dg, mode)
-    assert launches(0) == 0
-    assert launches(1, hh=300) == -capi.LB_ERR_PROB_SHAPE   # hidden % 256
-    assert launches(1, ii=1000) == -capi.LB_ERR_PROB_SHAPE  # intermediate % 128
-    assert launches(1, gg=64) == -capi.LB_ERR_PROB_SHAPE
-    assert launches(-1) == -capi.LB_ERR_ARG
-    assert launches(1, mode=3) == -capi.LB_ERR_ARG
-    assert launches(1, mode=2) == 2 and launches(4, mode=2) == 2
-    assert launches(1) == 2  # auto: two launches at batch 1
     ws = L.lb_marlin_mlp_fused_workspace_len(1, h, i)
     sb = L.lb_marlin_mlp_fused_scratch_bytes(1, h, i)
-    # the hand-off counters (1 + 2 * 64 lines) + each projection's counters; activations and [g | u] fit in scratch
-    assert ws >= 32 * 129 + 2 + (2 * i) // 256 and sb % 256 == 0 and sb >= 2 * i * 2
+    # each projection's counters; [g | u] (or the activations) then either launch's partials fit in scratch
+    assert ws >= 2 + (2 * i) // 256 and sb % 256 == 0 and sb >= 2 * i * 2
     assert L.lb_marlin_mlp_fused_scratch_bytes(0, h, i) == 0
     assert _mlp_fused(L, batch=0) == capi.LB_OK
     assert _mlp_fused(L, batch=-1) == capi.LB_ERR_ARG
-    assert _mlp_fused(L, mode=-1) == capi.LB_ERR_ARG
-    assert _mlp_fused(L, hidden=300) == capi.LB_ERR_PROB_SHAPE
+    assert _mlp_fused(L, hidden=300) == capi.LB_ERR_PROB_SHAPE   # hidden % 256
+    assert _mlp_fused(L, inter=1000) == capi.LB_ERR_PROB_SHAPE   # intermediate % 128
+    assert _mlp_fused(L, gg=64) == capi.LB_ERR_PROB_SHAPE
     assert _mlp_fused(L, x=None) == capi.LB_ERR_ARG
     assert _mlp_fused(L, x=MIS) == capi.LB_ERR_ALIGN
     assert _mlp_fused(L, ws_len=ws - 1) == capi.LB_ERR_WORKSPACE

@@ -97,14 +97,16 @@ def test_silu_packed_graph_replay(dev, m):
     _replay_and_check(torch, graph, [out], [eager], [ws], lambda: torch.cuda.synchronize())
 
 
-@pytest.mark.parametrize("batch", [1, 4])
+@pytest.mark.parametrize("batch", [1, 16])
 def test_mlp_fused_graph_replay(dev, batch):
-    """The one-launch MLP (its per-split ready counters live in the workspace)."""
+    """The decode MLP: the [g | u] round trip at batch 1, the gate/up launch
+    storing fp16(silu(g) * u) at batch 16 (both keep split counters in the
+    workspace)."""
     import torch
     from neurova_amd import capi
 
     h, it = 5120, 17408
-    print_case("graph-mlp", batch, capi.marlin_mlp_fused_launches(batch, h, it, 128, 128, capi.MLP_ONE_LAUNCH))
+    print_case("graph-mlp", batch)
     gen = torch.Generator(device=dev)
     gen.manual_seed(30 + batch)
     gq, gs = _marlin_tensors(torch, dev, h, 2 * it, gen)
@@ -115,7 +117,7 @@ def test_mlp_fused_graph_replay(dev, batch):
     out = torch.empty((batch, h), dtype=torch.float16, device=dev)
 
     def call(o):
-        assert capi.marlin_mlp_fused(x, gq, gs, dq, ds, o, h, it, 128, 128, ws, sc, mode=capi.MLP_ONE_LAUNCH) == 0
+        assert capi.marlin_mlp_fused(x, gq, gs, dq, ds, o, h, it, 128, 128, ws, sc) == 0
 
     call(out)
     torch.cuda.synchronize()

@@ -1,5 +1,7 @@
-"""The one-launch decode MLP (``lb_marlin_mlp_fused``) against the two
-projections it fuses, and against the oracle.
+"""The decode MLP entry point (``lb_marlin_mlp_fused``: the gate_up launch,
+storing fp16(silu(g) * u) where its decode tiles pair gate and up chunks, then
+the down launch) against the two projections it replaces, and against the
+oracle.
 
 The reference runs its production MLP as the gate_up projection followed by
 ``down.gemm_silu_packed`` (``adapters/qwen36_impl/model.py:1460-1470``,
@@ -67,7 +69,7 @@ def _two_launches(dev, x, gu_q, gu_s, d_q, d_s, hidden, inter, gg, dg):
     return to_np(out), to_np(mixed)
 
 
-def _fused(dev, x, gu_q, gu_s, d_q, d_s, hidden, inter, gg, dg, ws=None, mode=1):
+def _fused(dev, x, gu_q, gu_s, d_q, d_s, hidden, inter, gg, dg, ws=None):
     import torch
     from neurova_amd import capi
 
@@ -77,7 +79,7 @@ def _fused(dev, x, gu_q, gu_s, d_q, d_s, hidden, inter, gg, dg, ws=None, mode=1)
         ws = torch.zeros((capi.marlin_mlp_fused_workspace_len(batch, hidden, inter),), dtype=torch.int32, device=dev)
     scratch = torch.empty((capi.marlin_mlp_fused_scratch_bytes(batch, hidden, inter),), dtype=torch.uint8,
                           device=dev)
-    st = capi.marlin_mlp_fused(x, gu_q, gu_s, d_q, d_s, out, hidden, inter, gg, dg, ws, scratch, mode=mode)
+    st = capi.marlin_mlp_fused(x, gu_q, gu_s, d_q, d_s, out, hidden, inter, gg, dg, ws, scratch)
     assert st == 0, capi.status_string(st)
     torch.cuda.synchronize()
     assert int(ws.abs().sum()) == 0, f"workspace not left zero: {ws.nonzero().flatten()[:8].tolist()}"
@@ -92,44 +94,29 @@ CASES = [
     (512, 1024, 2, -1, 128),
     (512, 1024, 2, 128, -1),
     (256, 384, 5, 128, 128),
-    (512, 1024, 32, 128, 128),  # prefill kernels: two launches
+    (512, 1024, 32, 128, 128),  # prefill kernels: the [g | u] round trip
 ]
 
 
 @pytest.mark.parametrize("hidden,inter,batch,gg,dg", CASES)
 def test_fused_mlp_vs_two_launches_and_oracle(dev, hidden, inter, batch, gg, dg):
-    from neurova_amd import capi
-
-    print_case("mlp_fused", hidden, inter, batch, gg, dg,
-               "launches", capi.marlin_mlp_fused_launches(batch, hidden, inter, gg, dg, capi.MLP_ONE_LAUNCH))
+    print_case("mlp_fused", hidden, inter, batch, gg, dg)
     gu_q, gu_s, d_q, d_s, x = _problem(hidden, inter, batch, gg, dg, seed=batch + hidden)
     args = [to_dev(a, dev) for a in (x, gu_q, gu_s, d_q, d_s)]
-    got = _fused(dev, *args, hidden, inter, gg, dg, mode=capi.MLP_ONE_LAUNCH)
+    got = _fused(dev, *args, hidden, inter, gg, dg)
     ref, mixed = _two_launches(dev, *args, hidden, inter, gg, dg)
     assert np.array_equal(got.view(np.uint16), ref.view(np.uint16)), "fused != gate_up + silu-gated down"
-    for mode in (capi.MLP_AUTO, capi.MLP_TWO_LAUNCHES):
-        again = _fused(dev, *args, hidden, inter, gg, dg, mode=mode)
-        assert np.array_equal(again.view(np.uint16), ref.view(np.uint16)), mode
     # oracle: the gate_up projection, then the SiLU-gated down over the GPU's own [g | u]
     assert_close_f16(mixed, O.marlin_gemm(x, gu_q, gu_s, gg), what="gate_up")
     assert_close_f16(got, O.marlin_gemm_silu_packed(mixed, d_q, d_s, inter, dg), what="down(silu)")
 
 
 @pytest.mark.parametrize("batch", [1, 4, 16, 24, 32])
-def test_fused_mlp_model_shape_one_launch(dev, batch):
-    from neurova_amd import capi
-
-    launches = capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128, capi.MLP_ONE_LAUNCH)
-    print_case("mlp_fused_model", batch, "launches", launches)
-    # from batch 5: the two launches take direct-A and ring tiles the one-launch
-    # kernel does not have, so mode 1 runs them too (the gate_up launch storing
-    # the gated activations; the output stays bit-identical).  At batch 1-4 the
-    # gate_up call plans whole-K single-chunk tiles (two per CU, leftovers
-    # split), which the one launch does not have either; the one launch is
-    # covered at the smaller shapes above and at 4096 x 14336 below.
-    assert launches == 2
-    # auto: always the two launches (the one launch is opt-in)
-    assert capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128) == 2
+def test_fused_mlp_model_shape_vs_two_launches(dev, batch):
+    """At the model's shape: the [g | u] round trip at batch 1-4 (the gate_up
+    call plans whole-K single-chunk tiles), the gate_up launch storing the
+    gated activations from batch 5 on; bit-equal to the two projections."""
+    print_case("mlp_fused_model", batch)
     args = _problem_dev(HIDDEN, INTER, batch, 7 + batch, dev)
     got = _fused(dev, *args, HIDDEN, INTER, 128, 128)
     ref, _ = _two_launches(dev, *args, HIDDEN, INTER, 128, 128)
@@ -194,12 +181,10 @@ def _sample_cols(n, count, seed):
 
 @pytest.mark.parametrize("batch", [1, 4, 16, 32])
 def test_fused_mlp_model_shape_vs_oracle(dev, batch):
-    """The one-launch MLP at the model's shape (hidden 5120, intermediate
-    17408, g128) against the oracle, column-sampled: the gate_up stage on 16
-    chunks of its 34816 columns, the SiLU-gated down stage on 16 chunks of its
-    5120 outputs over the whole [g | u] row; and bit-equal to the two launches."""
-    from neurova_amd import capi
-
+    """The decode MLP at the model's shape (hidden 5120, intermediate 17408,
+    g128) against the oracle, column-sampled: the gate_up stage on 16 chunks of
+    its 34816 columns, the SiLU-gated down stage on 16 chunks of its 5120
+    outputs over the whole [g | u] row; and bit-equal to the two launches."""
     print_case("mlp_fused_model_oracle", batch)
     rng = np.random.default_rng(900 + batch)
     gu_q = rng.integers(-2**31, 2**31, size=(HIDDEN // 16, 4 * INTER), dtype=np.int64).astype(np.int32)
@@ -208,7 +193,7 @@ def test_fused_mlp_model_shape_vs_oracle(dev, batch):
     d_s = (np.abs(rng.normal(0, 0.01, (INTER // 128, HIDDEN))) + 1e-3).astype(np.float16)
     x = rng.normal(0, 1, (batch, HIDDEN)).astype(np.float16)
     args = [to_dev(a, dev) for a in (x, gu_q, gu_s, d_q, d_s)]
-    got = _fused(dev, *args, HIDDEN, INTER, 128, 128, mode=capi.MLP_ONE_LAUNCH)
+    got = _fused(dev, *args, HIDDEN, INTER, 128, 128)
     two, mixed = _two_launches(dev, *args, HIDDEN, INTER, 128, 128)
     assert np.array_equal(got.view(np.uint16), two.view(np.uint16))
     for n0, n1 in _sample_cols(2 * INTER, 16, batch):
@@ -218,38 +203,3 @@ def test_fused_mlp_model_shape_vs_oracle(dev, batch):
         assert_close_f16(got[:, n0:n1],
                          O.marlin_gemm_silu_packed(mixed, d_q[:, 2 * n0:2 * n1], d_s[:, n0:n1], INTER, 128),
                          what=f"down(silu) cols {n0}:{n1}")
-
-
-def test_fused_mlp_give_up_is_reported_and_recovers(dev):
-    """A one-launch wait that gives up (forced from the host with a spin limit
-    of one poll; every kernel still ends normally) is reported by
-    lb_marlin_mlp_fused_check and by the torch op's check=True, the workspace
-    is zeroed, and the next call is exact again."""
-    import torch
-    import langburst_cuda as lc
-    from neurova_amd import capi
-
-    # a shape whose two calls plan the staged tiles the one launch mirrors
-    batch, HIDDEN, INTER = 4, 4096, 14336
-    assert capi.marlin_mlp_fused_launches(batch, HIDDEN, INTER, 128, 128, capi.MLP_ONE_LAUNCH) == 1
-    print_case("mlp_fused_give_up", batch)
-    x, gu_q, gu_s, d_q, d_s = _problem_dev(HIDDEN, INTER, batch, 77, dev)
-    two, _ = _two_launches(dev, x, gu_q, gu_s, d_q, d_s, HIDDEN, INTER, 128, 128)
-    ws = torch.zeros((capi.marlin_mlp_fused_workspace_len(batch, HIDDEN, INTER),), dtype=torch.int32, device=dev)
-    scratch = torch.empty((capi.marlin_mlp_fused_scratch_bytes(batch, HIDDEN, INTER),), dtype=torch.uint8, device=dev)
-    out = torch.empty((batch, HIDDEN), dtype=torch.float16, device=dev)
-    try:
-        capi.marlin_mlp_fused_set_spin_limit(1)
-        assert capi.marlin_mlp_fused(x, gu_q, gu_s, d_q, d_s, out, HIDDEN, INTER, 128, 128, ws, scratch,
-                                     mode=capi.MLP_ONE_LAUNCH) == 0
-        assert capi.marlin_mlp_fused_check(ws) == capi.LB_ERR_HANDOFF
-        assert int(ws.abs().sum()) == 0
-        with pytest.raises(RuntimeError, match="gave up waiting"):
-            lc.lowbit_marlin_mlp_fused_out(gu_q, gu_s, d_q, d_s, x, out, ws, HIDDEN, INTER, 128, 128, mode=1,
-                                           check=True)
-        assert int(ws.abs().sum()) == 0
-    finally:
-        capi.marlin_mlp_fused_set_spin_limit(0)
-    lc.lowbit_marlin_mlp_fused_out(gu_q, gu_s, d_q, d_s, x, out, ws, HIDDEN, INTER, 128, 128, mode=1, check=True)
-    assert np.array_equal(to_np(out).view(np.uint16), two.view(np.uint16))
-    assert capi.marlin_mlp_fused_check(ws) == 0 and int(ws.abs().sum()) == 0

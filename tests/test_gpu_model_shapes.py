@@ -103,6 +103,43 @@ def test_decode_step_projection_vs_oracle(dev, name, k, n, silu, m):
         assert_close_f16(got[:, n0:n1], ref, what=f"{name} m={m} cols {n0}:{n1}")
 
 
+# The projections the reference publishes M = 1 timings for besides gate/up,
+# down and lm_head (langburst/docs/PERFORMANCE_LOG.md:421-427): K = 6144 has 48
+# scale groups, N = 14336 fewer 64-column chunks (224) than the device has CUs.
+PUBLISHED = [
+    ("attn_qkv", 5120, 14336),
+    ("gdn_qkvz", 5120, 16384),
+    ("gdn_out_attn_o", 6144, 5120),
+]
+
+
+@pytest.mark.parametrize("m", [1, 4])
+@pytest.mark.parametrize("name,k,n", PUBLISHED)
+def test_published_projection_vs_oracle(dev, name, k, n, m):
+    """The reference's other published projection shapes at decode batch
+    sizes, against the oracle on 12 sampled 64-column chunks, and with
+    per-column scales at M = 1."""
+    from neurova_amd import capi
+
+    plan = capi.marlin_describe_plan(m, n, k, 128)
+    print_case("published shape", name, m, k, n, plan["form"], plan["chunks_or_row_blocks"], plan["splits"])
+    seed = 100 + 10 * [sh[0] for sh in PUBLISHED].index(name) + m
+    qw, s, x = _inputs(m, k, n, seed=seed)
+    got = _gemm(dev, x, qw, s, 128)
+    assert np.isfinite(got.astype(np.float32)).all()
+    for n0, n1 in _chunks(n, 12, seed):
+        assert_close_f16(got[:, n0:n1], O.marlin_gemm(x, qw[:, 2 * n0:2 * n1], s[:, n0:n1], 128),
+                         what=f"{name} m={m} cols {n0}:{n1}")
+    if m == 1:
+        # (random scales stand for permuted ones; the permutation stays within
+        # 32-column blocks, so a 64-column slice is the slice's own layout)
+        qw1, s1, x1 = _inputs(m, k, n, seed=seed + 1, group=-1)
+        got1 = _gemm(dev, x1, qw1, s1, -1)
+        for n0, n1 in _chunks(n, 6, seed + 1):
+            ref = O.marlin_gemm(x1, qw1[:, 2 * n0:2 * n1], s1[:, n0:n1], -1)
+            assert_close_f16(got1[:, n0:n1], ref, what=f"{name} per-column m={m} cols {n0}:{n1}")
+
+
 @pytest.mark.parametrize("m", [1, 4])
 def test_lm_head_argmax_full_vocab(dev, m):
     """The fused argmax at the lm_head shape, K=5120, N=248320 (970 column

@@ -133,3 +133,21 @@ def test_plan_rejects_what_the_entry_points_reject(L):
     with pytest.raises(ValueError):
         _plan(1, 256, 256, g=64)
     assert _plan(0, 256, 256)["workgroups"] == 0
+
+
+# The decode projections of BASELINE.json configs[4] and the ones the reference
+# publishes timings for (langburst/docs/PERFORMANCE_LOG.md:421-427), K x N.
+NOALLOC_SHAPES = {"qkv": (5120, 7168), "o": (5120, 5120), "gate_up": (5120, 34816), "down": (17408, 5120),
+                  "attn_qkv": (5120, 14336), "gdn_qkvz": (5120, 16384), "gdn_out": (6144, 5120),
+                  "lm_head": (5120, 248320)}
+
+
+@pytest.mark.parametrize("name", sorted(NOALLOC_SHAPES))
+def test_noalloc_scratch_covers_decode_shapes(L, name):
+    """lb_marlin_gemm_noalloc's static scratch holds the partials of every plan
+    of these shapes up to M = 64 (the header's claim), grouped or per-column scales."""
+    k, n = NOALLOC_SHAPES[name]
+    limit = capi.marlin_noalloc_scratch_limit()
+    for m in range(1, 65):
+        for g in (128, -1):
+            assert capi.marlin_scratch_bytes(m, n, k, g) <= limit, (name, m, g)

@@ -239,3 +239,49 @@ def test_output_cache_policy(monkeypatch, policy, batch, cached):
     monkeypatch.setenv("LANGBURST_MARLIN_OUT_CACHE_POLICY", policy)
     monkeypatch.delenv("LANGBURST_MARLIN_OUT_CACHE_MAX_BATCH", raising=False)
     assert _OutputCache.wants(batch) is cached
+
+
+def test_output_cache_admits_before_allocating(monkeypatch):
+    """The cache decides admission before it allocates, as the reference does
+    (loader.py:254-302): with free memory exactly the minimum plus the new
+    buffer, the buffer is cached; checking after the allocation would count it
+    twice and refuse.  Device allocation and the free-memory query are mocked
+    (no GPU here); each mocked allocation lowers the free memory."""
+    import torch
+    from neurova_amd import store
+
+    mib = 1 << 20
+    out_bytes = 4 * 512 * 2  # batch 4 x 512 rows of fp16
+    ws_bytes = (512 // 128 * 16) * 4
+    free = {"bytes": 384 * mib + out_bytes}
+    real_empty, real_zeros = torch.empty, torch.zeros
+
+    def fake_alloc(real):
+        def alloc(shape, device=None, dtype=None):
+            t = real(shape, dtype=dtype)
+            if device is not None:
+                free["bytes"] -= t.numel() * t.element_size()
+            return t
+        return alloc
+
+    monkeypatch.setattr(torch, "empty", fake_alloc(real_empty))
+    monkeypatch.setattr(torch, "zeros", fake_alloc(real_zeros))
+    monkeypatch.setattr(torch.cuda, "mem_get_info", lambda device=None: (free["bytes"], 1 << 40))
+    monkeypatch.setenv("LANGBURST_MARLIN_OUT_CACHE_POLICY", "all")
+    monkeypatch.setenv("LANGBURST_MARLIN_CACHE_MAX_MIB", "0")
+    monkeypatch.setenv("LANGBURST_MARLIN_CACHE_MIN_FREE_MIB", "384")
+    monkeypatch.setattr(store._OutputCache, "bytes_used", 0)
+
+    class FakeQ:
+        device = torch.device("cuda", 0)
+        shape = (320, 1024)  # 512 rows
+
+    t = store.LowBitMarlinTensor("w", FakeQ(), None, 5120, 128)
+    out = t._cached(t._out_cache, 4, (4, 512), torch.float16)
+    assert t._out_cache.get(4) is out  # admitted at exactly the threshold
+    free["bytes"] = 384 * mib + ws_bytes
+    ws = t._cached_workspace()
+    assert t._workspace is ws
+    free["bytes"] = 384 * mib + out_bytes - 1  # one byte short: not cached
+    other = t._cached(t._out_cache, 8, (4, 512), torch.float16)
+    assert t._out_cache.get(8) is None and other is not out

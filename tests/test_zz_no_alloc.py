@@ -67,3 +67,103 @@ def test_noalloc_refuses_beyond_its_scratch(dev):
     assert capi.marlin_gemm_noalloc(a, b, c, s, ws, 128) == capi.LB_ERR_NOALLOC_LIMIT
     torch.cuda.synchronize()
     assert bool((c == 7.0).all()) and int(ws.abs().sum()) == 0
+
+
+def _capture_inputs(torch, dev, m, k, n, seed):
+    gen = torch.Generator(device=dev)
+    gen.manual_seed(seed)
+    q = torch.randint(-2 ** 31, 2 ** 31, (k // 16, 2 * n), dtype=torch.int32, device=dev, generator=gen)
+    s = (torch.randn((k // 128, n), device=dev, generator=gen) * 0.01).abs_().add_(1e-3).half()
+    x = torch.randn((m, k), device=dev, generator=gen).half()
+    return q, s, x
+
+
+def test_noalloc_graph_replay(dev):
+    """Two noalloc calls captured in one HIP graph (the second smaller), each
+    replay bit-equal to lb_marlin_gemm run eagerly, with eager work on the
+    same static scratch between the replays, the workspace zero after each."""
+    import torch
+    from neurova_amd import capi
+
+    shapes = [(1, 5120, 17408), (4, 1024, 2048)]
+    print_case("noalloc graph", shapes)
+    cases = []
+    for i, (m, k, n) in enumerate(shapes):
+        q, s, x = _capture_inputs(torch, dev, m, k, n, 60 + i)
+        ws = torch.zeros((n // 128 * 16,), dtype=torch.int32, device=dev)
+        ref = torch.empty((m, n), dtype=torch.float16, device=dev)
+        sc = torch.empty((max(1, capi.marlin_scratch_bytes(m, n, k, 128)),), dtype=torch.uint8, device=dev)
+        assert capi.marlin_gemm(x, q, ref, s, ws, 128, sc) == 0
+        cases.append((q, s, x, ws, ref, torch.empty((m, n), dtype=torch.float16, device=dev)))
+    torch.cuda.synchronize()
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):  # warm-up on the capture stream
+        for q, s, x, ws, _, out in cases:
+            assert capi.marlin_gemm_noalloc(x, q, out, s, ws, 128) == 0
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph, stream=side):
+        for q, s, x, ws, _, out in cases:
+            assert capi.marlin_gemm_noalloc(x, q, out, s, ws, 128) == 0
+    other = torch.empty_like(cases[0][5])
+    for rep in range(3):
+        for c in cases:
+            c[5].fill_(float("nan"))
+        graph.replay()
+        q, s, x, ws, _, _ = cases[0]
+        assert capi.marlin_gemm_noalloc(x, q, other, s, ws, 128) == 0  # eager use of the same scratch
+        torch.cuda.synchronize()
+        for q, s, x, ws, ref, out in cases:
+            assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), f"replay {rep}"
+            assert int(ws.abs().sum()) == 0
+
+
+_FIRST_CALL_IN_CAPTURE = r"""
+import sys
+import torch
+from neurova_amd import capi
+
+dev = torch.device("cuda:0")
+m, k, n = 1, 5120, 17408
+gen = torch.Generator(device=dev)
+gen.manual_seed(77)
+q = torch.randint(-2 ** 31, 2 ** 31, (k // 16, 2 * n), dtype=torch.int32, device=dev, generator=gen)
+s = (torch.randn((k // 128, n), device=dev, generator=gen) * 0.01).abs_().add_(1e-3).half()
+x = torch.randn((m, k), device=dev, generator=gen).half()
+ws = torch.zeros((n // 128 * 16,), dtype=torch.int32, device=dev)
+ref = torch.empty((m, n), dtype=torch.float16, device=dev)
+sc = torch.empty((capi.marlin_scratch_bytes(m, n, k, 128),), dtype=torch.uint8, device=dev)
+assert capi.marlin_gemm(x, q, ref, s, ws, 128, sc) == 0
+torch.cuda.synchronize()
+out = torch.empty((m, n), dtype=torch.float16, device=dev)
+side = torch.cuda.Stream()
+side.wait_stream(torch.cuda.current_stream())
+graph = torch.cuda.CUDAGraph()
+with torch.cuda.graph(graph, stream=side):
+    st = capi.marlin_gemm_noalloc(x, q, out, s, ws, 128)  # this process's first noalloc call
+assert st == 0, capi.status_string(st)
+for rep in range(3):
+    out.fill_(float("nan"))
+    graph.replay()
+    torch.cuda.synchronize()
+    assert torch.equal(out.view(torch.int16), ref.view(torch.int16)), rep
+    assert int(ws.abs().sum()) == 0
+print("first-call-in-capture ok", flush=True)
+"""
+
+
+def test_noalloc_first_call_inside_capture(dev):
+    """A fresh process whose first lb_marlin_gemm_noalloc call (the one that
+    looks up the static scratch's device address) is made inside a HIP graph
+    capture: the capture succeeds and every replay equals lb_marlin_gemm."""
+    import os
+    import subprocess
+    import sys
+
+    print_case("noalloc first call in capture")
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    proc = subprocess.run([sys.executable, "-c", _FIRST_CALL_IN_CAPTURE], cwd=root, capture_output=True, text=True,
+                          timeout=100)
+    assert proc.returncode == 0, proc.stdout[-2000:] + proc.stderr[-4000:]
+    assert "first-call-in-capture ok" in proc.stdout
