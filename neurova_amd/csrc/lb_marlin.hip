@@ -304,29 +304,32 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
   Plan pl;
   pl.n_cg = (int)(n / 256);
   const int groups = (int)(k / 128);
-  // Up to four rows of A, grouped scales, where the 64-column chunks number between one and two per CU:
-  // one single-chunk tile per CU over the whole K (its four waves' k shares
-  // summed in LDS, no split-K hand-off), and the leftover chunks split over K
-  // among at most one more workgroup per CU.  One whole-K single-chunk tile
-  // per CU measured 11.6 against 13.0 us at K = 5120, N = 16384, and the
-  // headline shape (N = 17408) 12.45 against 13.38 us.  With one scale per
-  // column it measured slower (13.7 against 12.6 us), so that keeps the split
-  // 4-chunk tiles (`allow_mixed` false).  At M = 2 and 3 (N = 17408) it measured
-  // 12.6 / 12.8 against 13.8 / 13.9 us; at M = 4 it gains where at most 4 chunks
-  // are left over (N = 16384: 12.5 against 13.6 us; K = 2048, N = 16640: 9.2
-  // against 10.1 us); with 16 left over it loses on 10 leftover splits (N = 17408:
-  // 14.2 against 13.9 us) and 4 (14.9 against 13.4) but gains on 6 (13.2 against
-  // 13.4 us; gate/up, N = 34816: 20.2 against 22.1 us), so M >= 4 caps the
-  // leftover splits at 6.
-  // Two whole-K tiles per CU where the chunks number two to 2 1/8 per CU
-  // (gate/up, N = 34816: 21.2 against 21.9 us; N = 33280: 19.6 against 21.4;
-  // K = 4096, N = 32768: 15.5 against 16.8 us); more per CU is not measured.
+  // Whole-K plan, up to four rows of A, grouped scales, K <= 5120, and between
+  // half a chunk (64 columns) and two chunks per CU: single-chunk tiles over
+  // the whole K (the four waves' k shares summed in LDS, no split-K hand-off),
+  // one or two per CU, and the chunks left over (at most CUs / 8) split over K
+  // among at most one more workgroup per CU.  Measured (one process, graph
+  // replay) against the split tiles: N = 16384 11.6 against 13.0 us, the
+  // headline N = 17408 12.45 against 13.38 (M = 2, 3: 12.6 / 12.8 against
+  // 13.8 / 13.9), gate/up N = 34816 21.2 against 21.9.  With one scale per
+  // column it was slower (13.7 against 12.6 us): `allow_mixed` false.  At M = 4
+  // 16 leftover chunks lose on 10 leftover splits (14.2 against 13.9 us) and
+  // gain on 6 (13.2 against 13.4; gate/up 20.2 against 22.1), so M = 4 caps
+  // the leftover splits at 6.
   if (m <= kMixedMaxM && allow_mixed && !argmax && am == gemm::A_PLAIN) {
     const int64_t chunks = n / 64, cus = device_cus();
     const int ksub = skinny::kWaves;  // 1-chunk tiles: the four waves share the k range
     // (measured at K <= 5120 and up to CUs / 8 leftover chunks; a longer K or
     // more leftover work per CU keeps the split tiles)
-    const int64_t per = std::min<int64_t>(chunks / cus, kMixedMaxPerCu), whole = per * cus;
+    int64_t per = std::min<int64_t>(chunks / cus, kMixedMaxPerCu), whole = per * cus;
+    // Fewer chunks than CUs but at least half as many: one whole-K tile per
+    // chunk and no split at all (K = 5120, M = 1: N = 14336 10.1 against 12.7
+    // us, N = 10240 9.7 against 10.9, N = 8192 9.6 against 10.1; below half,
+    // N = 7168 9.6 against 8.8 us, the split tiles stay).
+    if (per == 0 && chunks * 2 >= cus) {
+      per = 1;
+      whole = chunks;
+    }
     if (per >= 1 && (chunks - whole) * 8 <= cus && groups >= ksub && k <= 5120) {
       const int64_t left = chunks - whole;
       const int s = left > 0 ? (int)std::min<int64_t>(std::min<int64_t>(cus / left, groups / ksub), m >= 4 ? 6 : 256) : 1;
