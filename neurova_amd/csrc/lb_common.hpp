@@ -154,6 +154,12 @@ __device__ __forceinline__ int arrive(int* counter) {
   return __hip_atomic_fetch_add(counter, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Entry of a collect path, right after the branch on an arrival count: no
+// memory access of the collect may be moved above it (the partials are read
+// only once the count shows every split published; the hardware issues them
+// after the branch that needs the count).
+__device__ __forceinline__ void after_last_arrival() { asm volatile("" ::: "memory"); }
+
 // Zeroes a counter and waits for the swap to be performed.
 __device__ __forceinline__ void reset_counter(int* counter) {
   const int old = __hip_atomic_exchange(counter, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);

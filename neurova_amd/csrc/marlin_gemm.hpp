@@ -586,6 +586,7 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
     if (tid == 0) s_prev = arrive(ctr);
     __syncthreads();
     if (s_prev != nsplit - 1) return;
+    after_last_arrival();
     // The last arrival sums the splits in split order, one column block of
     // MB registers at a time.  Tiles below 128 rows: it reads its own split
     // back with the others, so that its registers are free for the loads, and
@@ -697,6 +698,7 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   if (tid == 0) s_prev = arrive(final_counter);
   __syncthreads();
   if (s_prev != p.n_cg * p.n_mb - 1) return;
+  after_last_arrival();
   for (int r = wave; r < p.m; r += kWaves) {
     uint64_t best = 0;
     for (int t = lane; t < p.n_cg; t += kWave)

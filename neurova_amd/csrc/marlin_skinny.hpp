@@ -257,6 +257,7 @@ __device__ __forceinline__ bool wave_epilogue(const Params& p, const f32x4 (&acc
   if (lane == 0) prev = arrive(ctr);
   prev = __builtin_amdgcn_readfirstlane(prev);
   if (prev != total - 1) return false;
+  after_last_arrival();
   if (lane == 0) __hip_atomic_store(ctr, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   if (MR == 1 && mrows <= 4) {
     // Few rows: lane = column, the 4 rows x 8 shares of 4-byte loads in flight
@@ -684,6 +685,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     if (tid == 0) s_prev = arrive(ctr);
     __syncthreads();
     if (s_prev != p.splits - 1) return false;  // not the last split of this tile
+    after_last_arrival();
     if (tid == 0) reset_counter(ctr);
     if constexpr (EPI == EPI_STORE) {  // every thread of the workgroup collects
       const int col0 = cg * 64 * cpw;
@@ -783,6 +785,7 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
   if (tid == 0) s_prev = arrive(final_counter);
   __syncthreads();
   if (s_prev != p.n_cg - 1) return false;
+  after_last_arrival();
   if (tid == 0) reset_counter(final_counter);
   for (int r = wave; r < mrows; r += kWaves) {
     uint64_t best = 0;
