@@ -112,10 +112,13 @@ size_t lb_marlin_scratch_bytes(int64_t prob_m, int64_t prob_n, int64_t prob_k, i
  * call would pass it.  Fills out[10]:
  *   [0] form: 0 decode tiles with the A slice staged whole, 1 decode tiles
  *       with A fragments loaded per step, 2 decode tiles with A through an
- *       LDS ring, 3 prefill GEMM tiles;
+ *       LDS ring, 3 prefill GEMM tiles with the split-tail schedule, 4 prefill
+ *       GEMM tiles with the stream-K schedule (every resident workgroup runs
+ *       an equal range of the tiles' scale-group stages);
  *   [1] decode: 64-column chunks per workgroup; prefill: 16-row blocks;
- *   [2] decode: k splits of every column tile; prefill: k splits of the tail tiles;
- *   [3] decode: 16-row MFMA blocks; prefill: whole tiles;
+ *   [2] decode: k splits of every column tile; split-tail: k splits of the
+ *       tail tiles; stream-K: 1;
+ *   [3] decode: 16-row MFMA blocks; split-tail: whole tiles; stream-K: 0;
  *   [4] workgroups; [5] dynamic LDS bytes per workgroup; [6] scratch bytes;
  *   [7] workspace entries used; [8] kernel launches; [9] compute units planned for.
  * Returns LB_OK, or the status the entry point would return for the shape. */

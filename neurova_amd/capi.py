@@ -119,7 +119,7 @@ def marlin_scratch_bytes(m, n, k, group_size) -> int:
 
 PLAN_FIELDS = ("form", "chunks_or_row_blocks", "splits", "row_blocks_or_full_tiles", "workgroups", "lds_bytes",
                "scratch_bytes", "workspace_entries", "launches", "cus")
-PLAN_FORMS = ("staged", "direct", "ring", "prefill")
+PLAN_FORMS = ("staged", "direct", "ring", "prefill", "prefill-streamk")
 
 
 def marlin_describe_plan(m, n, k, group_size, variant=0, workspace_len=None) -> dict:

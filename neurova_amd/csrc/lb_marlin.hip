@@ -168,6 +168,7 @@ struct Plan {
   int full_tiles = 0;   // GEMM: tiles computed whole
   int tail_tiles = 0;   // GEMM: tiles split over K ...
   int tail_splits = 1;  // ... this many ways
+  int sk_wgs = 0;       // GEMM: > 0, the stream-K schedule over this many workgroups
   int64_t wgs = 0;      // GEMM workgroups
   size_t lds = 0;    // decode kernel dynamic LDS
   size_t x_bytes = 0; // decode kernel: staged activations
@@ -407,6 +408,28 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
       full = tiles;
       tail = 0;
     }
+    // Stream-K where 128-row tiles fill between half of one round of the
+    // resident slots and all of it: every slot then runs the same number of
+    // stages, and a tile is cut only where a workgroup's range ends.  M = 2048,
+    // K = 17408, N = 5120 (320 tiles on 512 slots): 310 us against 321 us for
+    // 960 third-tiles (1.875 rounds).  With a full round or more the split tail
+    // stays ahead (K = 5120, N = 17408, 1088 tiles: 299 us against 323 us);
+    // unequal ranges, wave priorities falling with progress and one workgroup
+    // per CU were each slower (per-workgroup timestamps: the second workgroup
+    // on a CU runs its equal range 15-20 % slower than the first).  Two
+    // partial slots per workgroup.
+    const size_t sk_bytes = (size_t)2 * slots * 16 * pl.mb * gemm::kThreads * 4;
+    if (pl.mb == 8 && tiles < slots && tiles * 2 >= slots && workspace_len >= 1 + tiles &&
+        sk_bytes < ((size_t)1 << 31) && (int64_t)groups * tiles < ((int64_t)1 << 31)) {
+      pl.sk_wgs = (int)slots;
+      pl.full_tiles = 0;
+      pl.tail_tiles = (int)tiles;
+      pl.tail_splits = 1;
+      pl.wgs = slots;
+      pl.partial_bytes = align_up(sk_bytes);
+      pl.keys_bytes = align_up((size_t)m * (size_t)pl.n_cg * 8);
+      return pl;
+    }
     pl.full_tiles = (int)full;
     pl.tail_tiles = (int)tail;
     pl.tail_splits = s;
@@ -422,7 +445,7 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
 inline int64_t counters_needed(const Plan& pl, bool argmax) {
   // plain stores on wide tiles count per 64-column chunk (see skinny::wave_epilogue)
   if (pl.skinny && pl.splits > 1) return 1 + (int64_t)pl.n_cg * (argmax ? 1 : pl.cpw == skinny::kWaves ? pl.cpw : 1);
-  if (!pl.skinny && pl.tail_tiles > 0) return 1 + (int64_t)pl.tail_tiles;
+  if (!pl.skinny && pl.tail_tiles > 0) return 1 + (int64_t)pl.tail_tiles;  // stream-K: every tile
   return argmax ? 1 : 0;
 }
 
@@ -540,11 +563,21 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
   p.counters = workspace; p.partial = partial; p.tile_keys = keys;
   p.argmax_state = argmax_state; p.argmax_out = argmax_out;
   p.m = (int)m; p.n = (int)n; p.k = (int)k; p.grouped = grouped;
-  p.full_tiles = pl.full_tiles; p.tail_splits = pl.tail_splits; p.partial_bytes = (uint32_t)pl.partial_bytes;
+  p.full_tiles = pl.full_tiles; p.tail_splits = pl.tail_splits; p.sk_wgs = pl.sk_wgs;
+  p.partial_bytes = (uint32_t)pl.partial_bytes;
   p.kp_total = (int)(k / 32); p.n_cg = pl.n_cg; p.n_mb = pl.n_mb;
   dim3 grid((unsigned)pl.wgs, 1, 1);
-#define LB_GM(MBV, AMV, EPV, GV) \
-  hipLaunchKernelGGL((gemm::marlin_gemm_kernel<MBV, AMV, EPV, GV>), grid, dim3(gemm::kThreads), 0, st, p)
+#define LB_GM_SK(MBV, AMV, EPV, GV, SKV) \
+  hipLaunchKernelGGL((gemm::marlin_gemm_kernel<MBV, AMV, EPV, GV, SKV>), grid, dim3(gemm::kThreads), 0, st, p)
+#define LB_GM(MBV, AMV, EPV, GV)                                   \
+  do {                                                             \
+    if constexpr (MBV == 8 && AMV == gemm::A_PLAIN) {              \
+      if (pl.sk_wgs > 0) LB_GM_SK(MBV, AMV, EPV, GV, true);        \
+      else LB_GM_SK(MBV, AMV, EPV, GV, false);                     \
+    } else {                                                       \
+      LB_GM_SK(MBV, AMV, EPV, GV, false);                          \
+    }                                                              \
+  } while (0)
 #define LB_GM_G(MBV, AMV, EPV)                      \
   do {                                              \
     if (grouped) LB_GM(MBV, AMV, EPV, true);        \
@@ -565,6 +598,7 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
 #undef LB_GM_MB
 #undef LB_GM_G
 #undef LB_GM
+#undef LB_GM_SK
   return lbh::launch_status();
 }
 
@@ -624,7 +658,7 @@ extern "C" int lb_marlin_describe_plan(int64_t prob_m, int64_t prob_n, int64_t p
     out[4] = pl.whole > 0 ? pl.whole + (int64_t)(pl.n_cg - pl.whole) * pl.splits : (int64_t)pl.n_cg * pl.splits;
     out[5] = (int64_t)pl.lds;
   } else {
-    out[0] = 3;
+    out[0] = pl.sk_wgs > 0 ? 4 : 3;
     out[1] = pl.mb;
     out[2] = pl.tail_splits;
     out[3] = pl.full_tiles;

@@ -19,12 +19,16 @@
 // one s_waitcnt and one barrier end each stage.  The stage loop is unrolled by
 // two so that buffer and slot indices are compile-time constants.
 //
-// Schedule: the first `full_tiles` workgroups each compute one tile whole --
-// as many tiles as fill every resident slot a whole number of times -- and
-// the remaining tiles are split over K among `tail_splits` workgroups each, so
-// that the last partial round of tiles does not leave most CUs idle.  Split
-// workgroups publish fp32 partials to scratch; the last to arrive at the
-// tile's counter sums them in split order (deterministic) and finishes.
+// Schedules.  Stream-K: as many workgroups as are resident at once each take
+// an equal contiguous range of the (tile, scale group) stages in tile-major
+// order, so that no CU idles through a partial last round; a tile whose
+// stages span several workgroups is finished by the last of them to arrive.
+// Split-tail: the first `full_tiles` workgroups each compute one tile whole
+// -- as many tiles as fill every resident slot a whole number of times -- and
+// the remaining tiles are split over K among `tail_splits` workgroups each.
+// Either way, workgroups with part of a tile publish fp32 partials to
+// scratch; the last to arrive at the tile's counter sums them in k order
+// (deterministic) and finishes.
 
 #pragma once
 #include <type_traits>
@@ -55,6 +59,7 @@ struct Params {
   int grouped;
   int full_tiles;        // tiles computed whole, by workgroups 0 .. full_tiles - 1
   int tail_splits;       // the remaining tiles are split over K among this many workgroups each
+  int sk_wgs;            // > 0: stream-K schedule over this many workgroups (full_tiles, tail_splits unused)
   int kp_total;
   int n_cg;
   int n_mb;
@@ -101,7 +106,8 @@ __device__ __forceinline__ void pin_vgpr(T& x) {
   asm volatile("" : "+v"(x));
 }
 
-template <int MB, int AM, int EPI, bool GROUPED>
+// SK: the stream-K schedule (p.sk_wgs workgroups), else the split-tail one.
+template <int MB, int AM, int EPI, bool GROUPED, bool SK>
 __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kernel(Params p) {
   constexpr int BM = 16 * MB;
   // Plain A is staged by LDS DMA (buffer loads straight into LDS, no
@@ -133,30 +139,16 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  // work unit: a whole tile, or split `split` of a tail tile
-  // When every tile is split over K, each XCD (workgroups go to the 8 XCDs
-  // round-robin) takes a contiguous range of work units: a tile's splits and
-  // its neighbours share A rows and B columns in that XCD's L2 (measured 2-3 %
-  // faster there; slower by 10 % where whole tiles dominate, which keep the
-  // plain order).
-  int bid = blockIdx.x;
-  if (p.full_tiles == 0) {
-    const int w8 = (int)gridDim.x & ~7;
-    if (bid < w8) bid = (bid & 7) * (w8 >> 3) + (bid >> 3);
-  }
-  int tile = bid, split = 0, nsplit = 1;
-  if (bid >= p.full_tiles) {
-    nsplit = p.tail_splits;
-    const int u = bid - p.full_tiles;
-    tile = p.full_tiles + u / nsplit;
-    split = u - (u / nsplit) * nsplit;
-  }
+  const int groups = p.kp_total >> 2;
+
+  // One work unit: stages [st0, st0 + nst) of tile `tile`; `part`: not the
+  // whole tile (`split`: its index among the tile's splits under the
+  // split-tail schedule).
+  auto unit = [&](const int tile, const int st0, const int nst, const bool part, const int split)
+                  __attribute__((always_inline)) {
   const int mb = tile / p.n_cg;
   const int cg = tile - mb * p.n_cg;
   const int m0 = mb * BM;
-  const int groups = p.kp_total >> 2;
-  const int st0 = (int)(((int64_t)groups * split) / nsplit);           // first scale group (stage)
-  const int nst = (int)(((int64_t)groups * (split + 1)) / nsplit) - st0;  // stages of this unit
 
   const int chunk = cg * kWaves + wave;
   const uint32_t row_bytes = 8u * (uint32_t)p.n;
@@ -567,25 +559,51 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   const int rbase = m0 + 4 * (lane >> 4);
   const int ccol = chunk * 64 + (lane & 15);
 
-  if (nsplit > 1) {
-    // partials of tail tile t: [split][accumulator register q][thread], 16
-    // bytes each, so that one register of the workgroup is 4 KB contiguous
+  if (part) {
+    // A tile computed in parts.  Its contributors, in k order: `narr`
+    // workgroups, this one at position `own`.  Split-tail schedule: tail tile
+    // t's splits, partial slots t * S + split.  Stream-K: workgroup i owns two
+    // partial slots, 2i for the segment its range begins with and 2i + 1 for
+    // the one it ends with; a tile's contributors are consecutive workgroups
+    // i0 .. i1, where only i0 can reach the tile with its ending segment.
     constexpr int kQ = 4 * MB;
     constexpr uint32_t kRegBytes = kThreads * 16u;
-    const int t = tile - p.full_tiles;
+    int narr, own, ctr_idx, slot_base, first_alt = 0;
+    if constexpr (SK) {
+      const int64_t work = (int64_t)p.n_cg * p.n_mb * groups, wgs = p.sk_wgs;
+      const int64_t ts = (int64_t)tile * groups;
+      // the workgroup whose range holds stage s: the last i with i * work / wgs <= s
+      const int64_t i0 = ((ts + 1) * wgs - 1) / work;
+      const int64_t i1 = ((ts + groups) * wgs - 1) / work;
+      narr = (int)(i1 - i0 + 1);
+      own = (int)(blockIdx.x - i0);
+      first_alt = (i0 * work / wgs) < ts ? 1 : 0;
+      slot_base = 2 * (int)i0;
+      ctr_idx = 1 + tile;
+    } else {
+      narr = p.tail_splits;
+      own = split;
+      slot_base = (tile - p.full_tiles) * narr;
+      ctr_idx = 1 + tile - p.full_tiles;
+    }
+    // partial slot of contributor sp
+    auto slot_of = [&](int sp) __attribute__((always_inline)) -> uint32_t {
+      return SK ? (uint32_t)(slot_base + 2 * sp + (sp == 0 ? first_alt : 0)) : (uint32_t)(slot_base + sp);
+    };
     const __amdgpu_buffer_rsrc_t rp = buffer_of(p.partial, p.partial_bytes);
-    const uint32_t tile_off = (uint32_t)(t * nsplit) * kQ * kRegBytes + (uint32_t)tid * 16u;
+    const uint32_t lane_off = (uint32_t)tid * 16u;
+    const uint32_t own_off = slot_of(own) * (uint32_t)kQ * kRegBytes + lane_off;
 #pragma unroll
     for (int j = 0; j < 4; ++j)
 #pragma unroll
       for (int i = 0; i < MB; ++i)
-        publish16(rp, tile_off + (uint32_t)(split * kQ + j * MB + i) * kRegBytes, acc[j][i]);
+        publish16(rp, own_off + (uint32_t)(j * MB + i) * kRegBytes, acc[j][i]);
     wait_published();
     __syncthreads();
-    int32_t* ctr = p.counters + 1 + t;
+    int32_t* ctr = p.counters + ctr_idx;
     if (tid == 0) s_prev = arrive(ctr);
     __syncthreads();
-    if (s_prev != nsplit - 1) return;
+    if (s_prev != narr - 1) return;
     after_last_arrival();
     // The last arrival sums the splits in split order, one column block of
     // MB registers at a time.  Tiles below 128 rows: it reads its own split
@@ -604,31 +622,32 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
 #pragma unroll
       for (int i = 0; i < MB; ++i) sum[i] = (f32x4){0.f, 0.f, 0.f, 0.f};
       if constexpr (kReload) {
-        for (int sp0 = 0; sp0 < nsplit; sp0 += kCollect) {
+        for (int sp0 = 0; sp0 < narr; sp0 += kCollect) {
           f32x4 v[kCollect][MB];
 #pragma unroll
           for (int u = 0; u < kCollect; ++u)
-            if (sp0 + u < nsplit) {
+            if (sp0 + u < narr) {
+              const uint32_t off = slot_of(sp0 + u) * (uint32_t)kQ * kRegBytes + lane_off;
 #pragma unroll
-              for (int i = 0; i < MB; ++i)
-                v[u][i] = collect16(rp, tile_off + (uint32_t)((sp0 + u) * kQ + j * MB + i) * kRegBytes);
+              for (int i = 0; i < MB; ++i) v[u][i] = collect16(rp, off + (uint32_t)(j * MB + i) * kRegBytes);
             }
 #pragma unroll
           for (int u = 0; u < kCollect; ++u)
-            if (sp0 + u < nsplit) {
+            if (sp0 + u < narr) {
 #pragma unroll
               for (int i = 0; i < MB; ++i) sum[i] += v[u][i];
             }
         }
       } else {
-        for (int sp = 0; sp < nsplit; ++sp) {
-          if (sp == split) {
+        for (int sp = 0; sp < narr; ++sp) {
+          if (sp == own) {
 #pragma unroll
             for (int i = 0; i < MB; ++i) sum[i] += acc[j][i];
           } else {
+            const uint32_t off = slot_of(sp) * (uint32_t)kQ * kRegBytes + lane_off;
             f32x4 v[MB];
 #pragma unroll
-            for (int i = 0; i < MB; ++i) v[i] = collect16(rp, tile_off + (uint32_t)(sp * kQ + j * MB + i) * kRegBytes);
+            for (int i = 0; i < MB; ++i) v[i] = collect16(rp, off + (uint32_t)(j * MB + i) * kRegBytes);
 #pragma unroll
             for (int i = 0; i < MB; ++i) sum[i] += v[i];
           }
@@ -711,6 +730,43 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
     }
   }
   if (tid == 0) reset_counter(final_counter);
+  };
+
+  if constexpr (SK) {
+    // Stream-K: workgroup i takes stages [i * W / P, (i + 1) * W / P) of the
+    // W = tiles x groups stages in tile-major order, P = sk_wgs (every
+    // workgroup resident at once), and runs them tile segment by segment.
+    const int64_t work = (int64_t)p.n_cg * p.n_mb * groups;
+    const int64_t w1 = work * (blockIdx.x + 1) / p.sk_wgs;
+    for (int64_t w = work * blockIdx.x / p.sk_wgs; w < w1;) {
+      const int tile = (int)(w / groups);
+      const int st0 = (int)(w - (int64_t)tile * groups);
+      const int nst = (int)(w1 - w < (int64_t)(groups - st0) ? w1 - w : (int64_t)(groups - st0));
+      unit(tile, st0, nst, nst != groups, 0);
+      w += nst;
+    }
+  } else {
+  // Split-tail schedule.  When every tile is split over K, each XCD
+  // (workgroups go to the 8 XCDs round-robin) takes a contiguous range of
+  // work units: a tile's splits and its neighbours share A rows and B columns
+  // in that XCD's L2 (measured 2-3 % faster there; slower by 10 % where whole
+  // tiles dominate, which keep the plain order).
+  int bid = blockIdx.x;
+  if (p.full_tiles == 0) {
+    const int w8 = (int)gridDim.x & ~7;
+    if (bid < w8) bid = (bid & 7) * (w8 >> 3) + (bid >> 3);
+  }
+  int tile = bid, split = 0, nsplit = 1;
+  if (bid >= p.full_tiles) {
+    nsplit = p.tail_splits;
+    const int u = bid - p.full_tiles;
+    tile = p.full_tiles + u / nsplit;
+    split = u - (u / nsplit) * nsplit;
+  }
+  const int st0 = (int)(((int64_t)groups * split) / nsplit);           // first scale group (stage)
+  const int nst = (int)(((int64_t)groups * (split + 1)) / nsplit) - st0;  // stages of this unit
+  unit(tile, st0, nst, nsplit > 1, split);
+  }
 }
 
 }  // namespace gemm

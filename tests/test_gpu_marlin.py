@@ -200,13 +200,12 @@ def test_gemm_split_collect_vs_oracle(dev, m, k, n, group):
     assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
 
 
-@pytest.mark.parametrize("m,k,n,group", [(256, 5120, 17408, 128), (384, 17408, 5120, 128), (200, 16384, 4096, -1),
-                                         (2048, 17408, 5120, 128)])
+@pytest.mark.parametrize("m,k,n,group", [(256, 5120, 17408, 128), (384, 17408, 5120, 128), (200, 16384, 4096, -1)])
 def test_gemm_all_tiles_split_vs_oracle(dev, m, k, n, group):
-    """Fewer 128-row tiles than resident workgroups: every tile is split over
-    K (3 or 5 ways, up to 960 workgroups), a ragged last row block (M = 200),
-    both scale modes.  Sampled rows cover every tile; repeated launches are
-    bit-identical and the workspace is left zero."""
+    """Fewer 128-row tiles than half the resident workgroups: every tile is
+    split over K (3 or 5 ways), a ragged last row block (M = 200), both scale
+    modes.  Sampled rows cover every tile; repeated launches are bit-identical
+    and the workspace is left zero."""
     from neurova_amd import capi
 
     plan = capi.marlin_describe_plan(m, n, k, group)
@@ -218,6 +217,34 @@ def test_gemm_all_tiles_split_vs_oracle(dev, m, k, n, group):
     rows = rows[rows < m]
     exact = assert_close_f16(got[rows], O.marlin_gemm(x, qw, sp, group, rows=rows),
                              what=f"gemm-all-split m={m} k={k} n={n} g={group}")
+    assert exact > 0.9
+    again = _run_gemm(dev, x, qw, sp, group)
+    assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
+
+
+@pytest.mark.parametrize("m,k,n,group", [
+    (2048, 17408, 5120, 128),  # 320 tiles, 85 of 136 stages per workgroup
+    (1000, 1024, 8448, 128),   # ragged last row block; 4.125 stages per workgroup over 8-stage tiles
+    (1536, 2048, 8448, -1),    # per-column scales; 12.375 stages per workgroup over 16-stage tiles
+])
+def test_gemm_stream_k_vs_oracle(dev, m, k, n, group):
+    """The stream-K schedule (128-row tiles filling half to all of one round):
+    every resident workgroup runs an equal range of the tiles' scale-group
+    stages, and tiles cut between workgroups are finished by the last to
+    arrive, summing the parts in k order.  Sampled rows cover every row block
+    and every column; repeated launches are bit-identical; the workspace is
+    left zero."""
+    from neurova_amd import capi
+
+    plan = capi.marlin_describe_plan(m, n, k, group)
+    assert plan["form"] == "prefill-streamk" and plan["workgroups"] == 2 * plan["cus"], plan
+    print_case("gemm-stream-k", m, k, n, group)
+    codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=2600 + m + k)
+    got = _run_gemm(dev, x, qw, sp, group)
+    rows = np.unique(np.concatenate([np.arange(0, m, 61), [1, 127, 128, 129, m - 2, m - 1]]))
+    rows = rows[rows < m]
+    exact = assert_close_f16(got[rows], O.marlin_gemm(x, qw, sp, group, rows=rows),
+                             what=f"gemm-stream-k m={m} k={k} n={n} g={group}")
     assert exact > 0.9
     again = _run_gemm(dev, x, qw, sp, group)
     assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
@@ -368,7 +395,7 @@ def test_silu_packed_vs_oracle(dev, m):
 
 
 @pytest.mark.parametrize("m,k,n", [(1, 1024, 65536), (3, 512, 4096), (16, 256, 2048), (20, 1024, 65536), (32, 512, 4096),
-                                   (40, 512, 1024)])
+                                   (40, 512, 1024), (256, 512, 40960)])
 def test_argmax_vs_oracle(dev, m, k, n):
     import torch
     from neurova_amd import capi

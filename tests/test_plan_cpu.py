@@ -47,6 +47,13 @@ def test_plan_invariants(L, variant):
             assert p["chunks_or_row_blocks"] in (2, 4, 8), what
             assert p["launches"] == 1, what
             continue
+        if p["form"] == "prefill-streamk":
+            # 128-row tiles filling between half of one round of the resident slots and all of it
+            tiles, slots = -(-m // 128) * (n // 256), 2 * p["cus"]
+            assert m >= 128 and p["chunks_or_row_blocks"] == 8 and p["launches"] == 1, what
+            assert tiles < slots <= 2 * tiles and p["workgroups"] == slots, what
+            assert p["workspace_entries"] == 1 + tiles, what
+            continue
         cpw, s, mr = p["chunks_or_row_blocks"], p["splits"], p["row_blocks_or_full_tiles"]
         assert cpw in (1, 2, 4) and 1 <= s <= 256, what
         chunks, cus = n // 64, p["cus"]
@@ -107,11 +114,17 @@ def test_plan_rules_at_baseline_shapes(L):
     assert _plan(32, 34816, 5120)["form"] == "ring"
     assert _plan(32, 17408, 5120)["form"] in ("ring", "prefill")
     assert _plan(33, 7168, 5120)["form"] == "prefill"
-    # prefill (cfg3): 128-row tiles, tail tiles split over K
+    # prefill (cfg3): N = 17408, K = 5120: 1088 128-row tiles, 1024 whole, the tail split over K;
+    # N = 5120, K = 17408: 320 tiles on the stream-K schedule, one range per resident slot
     g = _plan(2048, 17408, 5120)
     assert (g["form"], g["chunks_or_row_blocks"], g["row_blocks_or_full_tiles"], g["splits"]) == ("prefill", 8, 1024, 3)
     g2 = _plan(2048, 5120, 17408)
-    assert (g2["form"], g2["row_blocks_or_full_tiles"], g2["splits"], g2["workgroups"]) == ("prefill", 0, 3, 960)
+    assert (g2["form"], g2["workgroups"], g2["scratch_bytes"]) == ("prefill-streamk", 512, 2 * 512 * 128 * 256 * 4)
+    # fewer tiles than half the slots: split tail; a whole number of rounds: whole tiles
+    t = _plan(256, 17408, 5120)
+    assert (t["form"], t["row_blocks_or_full_tiles"], t["splits"]) == ("prefill", 0, 3)
+    w = _plan(2048, 16384, 5120)
+    assert (w["form"], w["row_blocks_or_full_tiles"], w["splits"], w["workgroups"]) == ("prefill", 1024, 1, 1024)
     # lm_head argmax (N = 248320): staged tiles, one split
     a = _plan(1, 248320, 5120, variant=2)
     assert a["form"] == "staged" and a["workgroups"] >= 256

@@ -51,8 +51,9 @@ def test_noalloc_matches_caller_scratch(dev, shapes):
 
 
 def test_noalloc_refuses_beyond_its_scratch(dev):
-    """M = 2048, K = 17408, N = 5120 needs about 120 MiB of partials: refused
-    with LB_ERR_NOALLOC_LIMIT, nothing launched, the output untouched."""
+    """M = 2048, K = 17408, N = 5120 (the stream-K schedule, two 128 KiB partial
+    slots per resident workgroup) needs 128 MiB of partials: refused with
+    LB_ERR_NOALLOC_LIMIT, nothing launched, the output untouched."""
     import torch
     from neurova_amd import capi
 
