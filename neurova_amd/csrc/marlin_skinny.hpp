@@ -643,8 +643,64 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
         }
   }
   __syncthreads();
-  // Thread t < 64 * cpw owns column t of the tile: the sum of its k shares
-  // (the waves of chunk t / 64), in share order.
+
+  if constexpr (EPI == EPI_STORE) {
+    // Every thread takes one column of the tile and every kRG-th row: the sum
+    // of the column's k shares (the waves of its chunk), in share order, then
+    // the hand-off or the store.  (One wave per column set would issue all
+    // M rows' partial stores alone: at M = 32 that wave's 32 stores and their
+    // acknowledgements held the arrival up by about a microsecond.)
+    constexpr int kTileCols = 64 * cpw;
+    constexpr int kRG = kThreads / kTileCols;  // row groups: 4, 2, 1
+    constexpr int kPer = (kRows + kRG - 1) / kRG;
+    const int c = tid % kTileCols, rg = tid / kTileCols;
+    const int n = cg * kTileCols + c;
+    float v[kPer];
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int r = rg + i * kRG;
+      float t = 0.f;
+      if (r < mrows) {
+        t = tile[r * kCols + c];  // share 0
+        for (int ws = 1; ws < ksub; ++ws) t += tile[r * kCols + ws * kTileCols + c];
+      }
+      v[i] = t;
+    }
+    if (p.splits > 1) {
+      float* part = p.partial + (int64_t)split * p.m * p.n + n;
+#pragma unroll
+      for (int i = 0; i < kPer; ++i)
+        if (rg + i * kRG < mrows) publish(part + (int64_t)(rg + i * kRG) * p.n, v[i]);
+      wait_published();
+      __syncthreads();
+      int32_t* ctr = p.counters + 1 + cg;
+      if (tid == 0) s_prev = arrive(ctr);
+      __syncthreads();
+      if (s_prev != p.splits - 1) return false;  // not the last split of this tile
+      after_last_arrival();
+      if (tid == 0) reset_counter(ctr);
+      const int col0 = cg * kTileCols;  // every thread of the workgroup collects
+      collect_store<GROUPED, 16 * CPW, kThreads, kRows, 32>(
+          p, p.splits, col0, tid, [&](int row, int col, uint16_t v) { p.c[(int64_t)row * p.n + col0 + col] = v; });
+      return true;
+    }
+    // fp16 rounding (per-column scale after it, as the reference does)
+    f16 colscale = (f16)1.0f;
+    if (!GROUPED) colscale = __builtin_bit_cast(f16, p.s[per_column_scale_index(n)]);
+#pragma unroll
+    for (int i = 0; i < kPer; ++i) {
+      const int r = rg + i * kRG;
+      if (r < mrows) {
+        f16 h = (f16)v[i];
+        if (!GROUPED) h = h * colscale;
+        p.c[(int64_t)r * p.n + n] = __builtin_bit_cast(uint16_t, h);
+      }
+    }
+    return true;
+  }
+
+  // EPI_ACT, EPI_ARGMAX: thread t < 64 * cpw owns column t of the tile: the
+  // sum of its k shares (the waves of chunk t / 64), in share order.
   const bool col_live = tid < 64 * cpw;
   // this thread's output column
   const int n = EPI == EPI_ACT ? (col_live ? tile_chunk<EPI, CPW>(p, cg, tid >> 6) * 64 + (tid & 63) : 0)
@@ -687,12 +743,6 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     if (s_prev != p.splits - 1) return false;  // not the last split of this tile
     after_last_arrival();
     if (tid == 0) reset_counter(ctr);
-    if constexpr (EPI == EPI_STORE) {  // every thread of the workgroup collects
-      const int col0 = cg * 64 * cpw;
-      collect_store<GROUPED, 16 * CPW, kThreads, kRows, 32>(
-          p, p.splits, col0, tid, [&](int row, int col, uint16_t v) { p.c[(int64_t)row * p.n + col0 + col] = v; });
-      return true;
-    }
     if constexpr (EPI == EPI_ACT) {
       // every thread collects, the gate half and then the up half of the tile
       // (each a contiguous run of 32 CPW columns), into the LDS exchange
@@ -742,13 +792,6 @@ __device__ __forceinline__ bool skinny_tile(const Params p, const int cg, const 
     f16 h = (f16)v[r];
     if (!GROUPED) h = h * colscale;
     outh[r] = __builtin_bit_cast(uint16_t, h);
-  }
-
-  if (EPI == EPI_STORE) {
-#pragma unroll
-    for (int r = 0; r < kRows; ++r)
-      if (r < mrows && col_live) p.c[(int64_t)r * p.n + n] = outh[r];
-    return true;
   }
 
   if (EPI == EPI_ACT) {
