@@ -298,7 +298,9 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // pay below 5 rows.  M = 17..32: the direct form on 64-column tiles, the
 // ring on 4-chunk tiles; 2-chunk tiles go to the prefill kernel.
 constexpr int64_t kMixedMaxPerCu = 2;  // whole-K tiles per CU (more was not measured)
-constexpr int64_t kMixedMaxM = 4;      // rows (measured at M = 1..4)
+constexpr int64_t kMixedMaxM = 4;      // rows with the A slice staged (measured at M = 1..4)
+constexpr int64_t kMixedDirectMaxM = 32;    // rows with A loaded per step, one whole-K tile per CU
+constexpr int64_t kMixedDirectMaxM2 = 8;    // ... and with two whole-K tiles per CU
 
 inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, int am, bool argmax = false,
                       bool allow_mixed = true) {
@@ -316,9 +318,17 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
   // column it was slower (13.7 against 12.6 us): `allow_mixed` false.  At M = 4
   // 16 leftover chunks lose on 10 leftover splits (14.2 against 13.9 us) and
   // gain on 6 (13.2 against 13.4; gate/up 20.2 against 22.1), so M = 4 caps
-  // the leftover splits at 6.
-  if (m <= kMixedMaxM && allow_mixed && !argmax && am == gemm::A_PLAIN) {
-    const int64_t chunks = n / 64, cus = device_cus();
+  // the leftover splits at 6.  M = 5..32: the same tiles with A loaded per step
+  // (the direct form; the slice no longer fits LDS), where the chunks give every
+  // CU one whole-K tile (N = 17408: M = 8 12.4 against 14.1 us, M = 16 15.0
+  // against 16.0, M = 32 22.2 against 23.7 on the split tiles) or two up to
+  // M = 8 (N = 34816, M = 8: 20.9 against 22.6 us; M = 16 even, M = 32 39.2
+  // against 31.2 on the ring tiles).
+  const int64_t chunks_all = n / 64, cus_all = device_cus();
+  const bool mixed_direct = m > kMixedMaxM && m <= kMixedDirectMaxM && chunks_all >= cus_all &&
+                            (chunks_all < 2 * cus_all || m <= kMixedDirectMaxM2);
+  if ((m <= kMixedMaxM || mixed_direct) && allow_mixed && !argmax && am == gemm::A_PLAIN) {
+    const int64_t chunks = chunks_all, cus = cus_all;
     const int ksub = skinny::kWaves;  // 1-chunk tiles: the four waves share the k range
     // (measured at K <= 5120 and up to CUs / 8 leftover chunks; a longer K or
     // more leftover work per CU keeps the split tiles)
@@ -336,14 +346,14 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
       const int s = left > 0 ? (int)std::min<int64_t>(std::min<int64_t>(cus / left, groups / ksub), m >= 4 ? 6 : 256) : 1;
       if (left == 0 || (s >= 2 && workspace_len >= 1 + chunks)) {
         pl.skinny = true;
-        pl.direct = false;
-        pl.mr = 1;
+        pl.direct = mixed_direct;
+        pl.mr = mixed_direct ? (int)((m + 15) / 16) : 1;
         pl.cpw = 1;
         pl.n_cg = (int)chunks;
         pl.whole = (int)whole;
         pl.splits = s;
-        pl.x_bytes = (size_t)groups * 128 * (size_t)m * 2;
-        pl.lds = std::max(pl.x_bytes + 16, (size_t)m * skinny::kCols * 4);
+        pl.x_bytes = mixed_direct ? 0 : (size_t)groups * 128 * (size_t)m * 2;
+        pl.lds = std::max(mixed_direct ? 0 : pl.x_bytes + 16, (size_t)m * skinny::kCols * 4);
         pl.partial_bytes = left > 0 ? align_up((size_t)s * (size_t)m * (size_t)n * 4) : 0;
         pl.keys_bytes = align_up((size_t)m * (size_t)pl.n_cg * 8);
         return pl;
@@ -503,8 +513,10 @@ int run(Variant var, const uint16_t* a, const int32_t* b, uint16_t* c, const uin
                          (int)m, (int)k);
       av = act;
     }
-    const int32_t sp = pl.splits;
-    dim3 grid((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
+    // (mixed plans: the whole-K tile count rides in the high bits of the split count)
+    const int32_t sp = pl.whole > 0 ? (int32_t)((pl.whole << 16) | pl.splits) : pl.splits;
+    const dim3 grid = pl.whole > 0 ? dim3((unsigned)(pl.whole + (int64_t)(pl.n_cg - pl.whole) * pl.splits), 1, 1)
+                                   : dim3((unsigned)pl.n_cg, (unsigned)pl.splits, 1);
 #define LB_SKD(AMV, GV, CV, MRV)                                                                                  \
   hipLaunchKernelGGL((skinny::marlin_skinny_kernel<AMV, skinny::EPI_STORE, GV, CV, MRV>), grid,                  \
                      dim3(skinny::kThreads), pl.lds, st, av, reinterpret_cast<const uint32_t*>(b), s, (int)m, (int)n, \
@@ -798,8 +810,12 @@ int64_t fused_counters(const marlin::Plan& pl) {
 
 FusedMlpPlan fused_mlp_plan(int64_t batch, int64_t hidden, int64_t inter, bool g1, bool g2) {
   FusedMlpPlan p;
-  // as run() plans each projection (the mixed decode plan only with grouped scales)
-  p.up = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN, false, g1);
+  // as run() plans each projection (the mixed decode plan only with grouped
+  // scales), except that from M = 5 the gate/up launch keeps the 2- or 4-chunk
+  // tiles that can pair gate and up chunks (its SiLU-gated store saves the
+  // down launch's separate gating pass)
+  p.up = marlin::make_plan(batch, 2 * inter, hidden, INT64_MAX, gemm::A_PLAIN, false,
+                           g1 && batch <= marlin::kMixedMaxM);
   p.down = marlin::make_plan(batch, hidden, inter, INT64_MAX, gemm::A_SILU_PACKED, false, g2);
   // decode tiles of 2 or 4 chunks pair gate and up chunks; single-chunk tiles
   // and prefill tiles take the [g | u] round trip

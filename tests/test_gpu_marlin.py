@@ -133,9 +133,9 @@ def test_wide_decode_vs_oracle(dev, m, k, group):
 def test_wide_decode_leftovers_vs_oracle(dev, m, k, n, group):
     """Decode at N just above 64 columns per CU (16384): 256-column tiles that
     do not divide evenly over the CUs, up to M = 8, both scale modes, and
-    repeated launches bit-identical.  The grouped cases at M <= 4 take the
-    mixed plan (one or two whole-K single-chunk tiles per CU, leftover chunks
-    split)."""
+    repeated launches bit-identical.  The grouped cases take the mixed plan
+    (one or two whole-K single-chunk tiles per CU, leftover chunks split): A
+    staged at M <= 4, loaded per step at M = 8."""
     print_case("wide-left", m, k, n, group)
     codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=900 + m + k + n)
     got = _run_gemm(dev, x, qw, sp, group)
@@ -148,6 +148,37 @@ def test_wide_decode_leftovers_vs_oracle(dev, m, k, n, group):
         assert_reference_rounding(got, ref, x, qw, sp, group, what=f"wide-left m={m} k={k} n={n}")
     # repeated launches are bit-identical (split partials are summed in split order)
     again = _run_gemm(dev, x, qw, sp, group)
+    assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
+
+
+@pytest.mark.parametrize("m,k,n", [
+    (5, 5120, 17408),   # one whole-K tile per CU, 16 leftover chunks split 6 ways
+    (13, 2048, 17408),
+    (20, 5120, 16640),  # two 16-row MFMA blocks, rows 20..31 masked; 4 leftover chunks
+    (32, 1024, 17408),
+    (8, 2048, 34816),   # two whole-K tiles per CU
+    (7, 1024, 33024),   # eight k groups: two per wave, the leftover chunks split 2 ways
+    (16, 5120, 16384),  # whole-K tiles only, no leftover
+])
+def test_mixed_direct_vs_oracle(dev, m, k, n):
+    """The mixed whole-K plan with A loaded per step (M = 5..32): single-chunk
+    tiles over the whole K, one per CU (two up to M = 8), their four waves' k
+    shares summed in LDS, the leftover chunks split over K; ragged M in both
+    16-row blocks; repeated launches bit-identical."""
+    from neurova_amd import capi
+
+    plan = capi.marlin_describe_plan(m, n, k, 128)
+    chunks = n // 64
+    assert plan["form"] == "direct" and plan["chunks_or_row_blocks"] == 1, plan
+    assert plan["row_blocks_or_full_tiles"] == (m + 15) // 16, plan
+    assert plan["workgroups"] != chunks * plan["splits"] or chunks == plan["cus"], plan
+    print_case("mixed-direct", m, k, n)
+    codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=950 + m + k + n)
+    got = _run_gemm(dev, x, qw, sp, 128)
+    ref = O.marlin_gemm(x, qw, sp, 128)
+    assert_close_f16(got, ref, what=f"mixed-direct m={m} k={k} n={n}")
+    assert_reference_rounding(got, ref, x, qw, sp, 128, what=f"mixed-direct m={m} k={k} n={n}")
+    again = _run_gemm(dev, x, qw, sp, 128)
     assert np.array_equal(got.view(np.uint16), again.view(np.uint16))
 
 

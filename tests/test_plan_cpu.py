@@ -57,11 +57,18 @@ def test_plan_invariants(L, variant):
         cpw, s, mr = p["chunks_or_row_blocks"], p["splits"], p["row_blocks_or_full_tiles"]
         assert cpw in (1, 2, 4) and 1 <= s <= 256, what
         chunks, cus = n // 64, p["cus"]
-        if cpw == 1 and m <= 4 and p["workgroups"] != chunks * s:
-            # mixed: one whole-K single-chunk tile per CU, the leftover chunks split s ways
-            whole = min(chunks // cus, 2) * cus  # one or two whole-K tiles per CU
-            assert p["form"] == "staged" and cus < chunks and (chunks - whole) * 8 <= cus and k <= 5120, what
-            assert m <= 3 or s <= 6, what  # M = 4: at most 6 leftover splits
+        if cpw == 1 and p["workgroups"] != chunks * s:
+            # mixed: one or two whole-K single-chunk tiles per CU, the leftover chunks split s ways;
+            # A staged up to M = 4, loaded per step (direct) for M = 5..32 with one whole-K tile
+            # per CU, or two up to M = 8
+            whole = min(chunks // cus, 2) * cus
+            assert cus < chunks and (chunks - whole) * 8 <= cus and k <= 5120, what
+            if m <= 4:
+                assert p["form"] == "staged", what
+            else:
+                assert p["form"] == "direct" and m <= 32 and (chunks < 2 * cus or m <= 8), what
+                assert p["row_blocks_or_full_tiles"] == (m + 15) // 16, what
+            assert m <= 3 or s <= 6, what  # M >= 4: at most 6 leftover splits
             assert p["workgroups"] == whole + (chunks - whole) * s, what
         else:
             assert p["workgroups"] == (n // (64 * cpw)) * s, what
@@ -112,7 +119,14 @@ def test_plan_rules_at_baseline_shapes(L):
     # M = 17..32: 64-column direct tiles, the ring on 4-chunk tiles, 2-chunk tiles to the prefill kernel
     assert _plan(32, 7168, 5120)["form"] == "direct"
     assert _plan(32, 34816, 5120)["form"] == "ring"
-    assert _plan(32, 17408, 5120)["form"] in ("ring", "prefill")
+    # N = 17408 at M = 5..32: one whole-K single-chunk tile per CU, A loaded per step, the 16
+    # leftover chunks split 6 ways
+    h = _plan(32, 17408, 5120)
+    assert (h["form"], h["chunks_or_row_blocks"], h["row_blocks_or_full_tiles"], h["splits"], h["workgroups"]) == \
+        ("direct", 1, 2, 6, 256 + 16 * 6)
+    assert _plan(16, 17408, 5120)["workgroups"] == 256 + 16 * 6
+    # two whole-K tiles per CU only up to M = 8 (gate/up)
+    assert _plan(8, 34816, 5120)["workgroups"] == 512 + 32 * 6 and _plan(9, 34816, 5120)["form"] != "direct"
     assert _plan(33, 7168, 5120)["form"] == "prefill"
     # prefill (cfg3): N = 17408, K = 5120: 1088 128-row tiles, 1024 whole, the tail split over K;
     # N = 5120, K = 17408: 320 tiles on the stream-K schedule, one range per resident slot
