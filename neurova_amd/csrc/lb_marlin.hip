@@ -319,13 +319,15 @@ inline Plan make_plan(int64_t m, int64_t n, int64_t k, int64_t workspace_len, in
   // 16 leftover chunks lose on 10 leftover splits (14.2 against 13.9 us) and
   // gain on 6 (13.2 against 13.4; gate/up 20.2 against 22.1), so M = 4 caps
   // the leftover splits at 6.  M = 5..32: the same tiles with A loaded per step
-  // (the direct form; the slice no longer fits LDS), where the chunks give every
-  // CU one whole-K tile (N = 17408: M = 8 12.4 against 14.1 us, M = 16 15.0
-  // against 16.0, M = 32 22.2 against 23.7 on the split tiles) or two up to
-  // M = 8 (N = 34816, M = 8: 20.9 against 22.6 us; M = 16 even, M = 32 39.2
-  // against 31.2 on the ring tiles).
+  // (the direct form; the slice no longer fits LDS), where the chunks give at
+  // least 5/8 of the CUs one whole-K tile (N = 17408: M = 8 12.4 against 14.1
+  // us, M = 16 15.0 against 16.0, M = 32 22.2 against 23.7 on the split tiles;
+  // N = 14336: M = 8 10.5 against 13.5, M = 32 17.6 against 24.6; N = 10240:
+  // M = 16 11.5 against 12.5; at half, N = 8192, M = 32 18.3 against 14.3) or
+  // two per CU up to M = 8 (N = 34816, M = 8: 20.9 against 22.6 us; M = 16 even,
+  // M = 32 39.2 against 31.2 on the ring tiles).
   const int64_t chunks_all = n / 64, cus_all = device_cus();
-  const bool mixed_direct = m > kMixedMaxM && m <= kMixedDirectMaxM && chunks_all >= cus_all &&
+  const bool mixed_direct = m > kMixedMaxM && m <= kMixedDirectMaxM && chunks_all * 8 >= cus_all * 5 &&
                             (chunks_all < 2 * cus_all || m <= kMixedDirectMaxM2);
   if ((m <= kMixedMaxM || mixed_direct) && allow_mixed && !argmax && am == gemm::A_PLAIN) {
     const int64_t chunks = chunks_all, cus = cus_all;

@@ -159,19 +159,22 @@ def test_wide_decode_leftovers_vs_oracle(dev, m, k, n, group):
     (8, 2048, 34816),   # two whole-K tiles per CU
     (7, 1024, 33024),   # eight k groups: two per wave, the leftover chunks split 2 ways
     (16, 5120, 16384),  # whole-K tiles only, no leftover
+    (8, 5120, 14336),   # 224 chunks: one whole-K tile each, 32 CUs idle
+    (29, 2048, 10240),  # 160 chunks
 ])
 def test_mixed_direct_vs_oracle(dev, m, k, n):
     """The mixed whole-K plan with A loaded per step (M = 5..32): single-chunk
-    tiles over the whole K, one per CU (two up to M = 8), their four waves' k
-    shares summed in LDS, the leftover chunks split over K; ragged M in both
-    16-row blocks; repeated launches bit-identical."""
+    tiles over the whole K, at most one per CU (two up to M = 8), their four
+    waves' k shares summed in LDS, the leftover chunks split over K; ragged M
+    in both 16-row blocks; repeated launches bit-identical."""
     from neurova_amd import capi
 
     plan = capi.marlin_describe_plan(m, n, k, 128)
-    chunks = n // 64
+    chunks, cus = n // 64, plan["cus"]
     assert plan["form"] == "direct" and plan["chunks_or_row_blocks"] == 1, plan
     assert plan["row_blocks_or_full_tiles"] == (m + 15) // 16, plan
-    assert plan["workgroups"] != chunks * plan["splits"] or chunks == plan["cus"], plan
+    whole = min(chunks // cus, 2) * cus if chunks >= cus else chunks
+    assert plan["workgroups"] == whole + (chunks - whole) * plan["splits"], plan
     print_case("mixed-direct", m, k, n)
     codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=950 + m + k + n)
     got = _run_gemm(dev, x, qw, sp, 128)
