@@ -269,6 +269,18 @@ inline Tiling staged_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // A), else the one with the most workgroups.
 inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
   Tiling t;
+  // M = 17..32 with fewer 64-column chunks than CUs: single-chunk tiles split to
+  // about one workgroup per CU (M = 32, K = 5120: N = 5120 11.6 against 12.6 us
+  // at 2 per CU, 14.2 at 1.5 per CU; K = 17408, N = 5120: 22.3 against 23.5;
+  // N = 7168 even)
+  if (m > skinny::kMaxM && n / 64 < device_cus() && k / 128 >= skinny::kWaves) {
+    const int64_t tiles = n / 64;
+    int s = (int)std::max<int64_t>(1, device_cus() / tiles);
+    s = std::min<int>(s, (int)std::max<int64_t>(1, k / (32 * m)));  // partials within half the weight bytes
+    s = std::min<int>(s, (int)(k / 128 / skinny::kWaves));  // every wave a scale group
+    if (workspace_len < 1 + tiles) s = 1;
+    return Tiling{1, s};
+  }
   int64_t most = -1;
   for (int c = skinny::kWaves; c >= 1; c /= 2) {
     const int sc = skinny_splits(m, n, k, workspace_len, c, true);
