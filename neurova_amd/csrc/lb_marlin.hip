@@ -269,11 +269,14 @@ inline Tiling staged_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // A), else the one with the most workgroups.
 inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_len) {
   Tiling t;
-  // M = 17..32 with fewer 64-column chunks than CUs: single-chunk tiles split to
-  // about one workgroup per CU (M = 32, K = 5120: N = 5120 11.6 against 12.6 us
-  // at 2 per CU, 14.2 at 1.5 per CU; K = 17408, N = 5120: 22.3 against 23.5;
-  // N = 7168 even)
-  if (m > skinny::kMaxM && n / 64 < device_cus() && k / 128 >= skinny::kWaves) {
+  // From M = 12 (M = 8 at long K) with fewer 64-column chunks than CUs:
+  // single-chunk tiles split to about one workgroup per CU instead of two
+  // (M = 32, K = 5120: N = 5120 11.6 against 12.6 us, 14.2 at 1.5 per CU;
+  // K = 17408, N = 5120: 22.3 against 23.5; M = 16: 15.2 against 16.3, N = 7168
+  // 9.8 against 10.1; M = 12 even at K = 5120, 14.3 against 15.1 at K = 17408;
+  // M = 8: 13.6 against 14.1 at K = 17408, 0.3 us slower at K = 5120, as at M
+  // = 1 and 4)
+  if ((m >= 12 || (m >= 8 && k > 8192)) && n / 64 < device_cus() && k / 128 >= skinny::kWaves) {
     const int64_t tiles = n / 64;
     int s = (int)std::max<int64_t>(1, device_cus() / tiles);
     s = std::min<int>(s, (int)std::max<int64_t>(1, k / (32 * m)));  // partials within half the weight bytes
