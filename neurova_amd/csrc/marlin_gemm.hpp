@@ -144,8 +144,14 @@ __global__ __launch_bounds__(kThreads, wgs_per_cu(MB, AM)) void marlin_gemm_kern
   // One work unit: stages [st0, st0 + nst) of tile `tile`; `part`: not the
   // whole tile (`split`: its index among the tile's splits under the
   // split-tail schedule).
-  auto unit = [&](const int tile, const int st0, const int nst, const bool part, const int split)
+  auto unit = [&](const int tile_in, const int st0_in, const int nst_in, const bool part, const int split_in)
                   __attribute__((always_inline)) {
+  // wave-uniform (the compiler's uniformity analysis does not follow them
+  // through the lambda: without this the stage offsets go through VGPRs)
+  const int tile = __builtin_amdgcn_readfirstlane(tile_in);
+  const int st0 = __builtin_amdgcn_readfirstlane(st0_in);
+  const int nst = __builtin_amdgcn_readfirstlane(nst_in);
+  const int split = __builtin_amdgcn_readfirstlane(split_in);
   const int mb = tile / p.n_cg;
   const int cg = tile - mb * p.n_cg;
   const int m0 = mb * BM;
