@@ -310,8 +310,9 @@ inline Tiling direct_tiling(int64_t m, int64_t n, int64_t k, int64_t workspace_l
 // workgroups (on 4-chunk tiles, A then goes through the LDS ring); the
 // staged form where 4-chunk tiles share the slice.  The SiLU-gated direct
 // form first forms fp16(silu(g) * u) in a launch of its own, which does not
-// pay below 5 rows.  M = 17..32: the direct form on 64-column tiles, the
-// ring on 4-chunk tiles; 2-chunk tiles go to the prefill kernel.
+// pay below 5 rows.  M = 17..32: the direct form on 64-column tiles (whole-K
+// tiles where the chunks cover the CUs, below that about one workgroup per
+// CU), the ring on 4-chunk tiles; 2-chunk tiles go to the prefill kernel.
 constexpr int64_t kMixedMaxPerCu = 2;  // whole-K tiles per CU (more was not measured)
 constexpr int64_t kMixedMaxM = 4;      // rows with the A slice staged (measured at M = 1..4)
 constexpr int64_t kMixedDirectMaxM = 32;    // rows with A loaded per step, one whole-K tile per CU

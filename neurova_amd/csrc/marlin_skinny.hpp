@@ -31,23 +31,30 @@
 // reference's fp16 (q - 8) * s, rounded as marlin_cuda_kernel.cu:131-159
 // rounds it; the MFMA then accumulates exact products in fp32.
 //
-// Latency.  M <= 16: the activation slice of the workgroup's k range is
-// staged once in LDS in fragment order ([k/32][4 k-groups][m] x 16 bytes,
-// SiLU-gated variant: fp16(silu(g) * u)); the staging loads are issued first
-// and the first weight batches (one scale group, 1 KB per wave each) right
-// behind them, so the staging round trip overlaps the weight fetch.  A ring
-// of kDepth batches stays in flight, with unconditional loads, so the memory
-// counters never force a full drain.  M = 17..32 (A_DIRECT, MR = 2 row blocks
-// of 16): staging the whole slice would hold every wave at the barrier for
-// twice the weight bytes, so each lane loads its own A fragments (16 bytes
-// per row block and step, from L2, completed by a lane swap) with the weight
-// batch they meet, in the same ring; no LDS, no barrier before the loop.
+// Latency.  A ring of kDepth weight batches (one scale group, 1 KB per wave
+// each) stays in flight, with unconditional loads, so the memory counters
+// never force a full drain.  The A operand comes one of three ways (the host
+// planner picks per shape):
+//   staged (M <= 16): the activation slice of the workgroup's k range is
+//     staged once in LDS in fragment order ([k/32][4 k-groups][m] x 16 bytes,
+//     SiLU-gated variant: fp16(silu(g) * u)); the staging loads are issued
+//     first and the first weight batches right behind them, so the staging
+//     round trip overlaps the weight fetch;
+//   direct (narrow tiles, and M = 5..32 whole-K tiles; MR = 2 row blocks of 16
+//     above 16 rows): each lane loads its own A fragments (16 bytes per row
+//     block and step, from L2, completed by a lane swap) with the weight batch
+//     they meet, in the same ring; no LDS, no barrier before the loop;
+//   ring (4-chunk tiles, M <= 32): one scale group of A at a time through a
+//     two-slot LDS ring shared by the four waves.
 
-// Epilogue.  Accumulators go through LDS so that thread t owns output column
-// t of the workgroup's 256.  Under split-K each workgroup publishes fp32
-// partials to scratch [S][M][N]; the last one to arrive on the tile's counter
-// (workspace, zero on entry and on exit) collects them in split order
-// (deterministic), rounds to fp16 and stores or feeds the fused argmax.
+// Epilogue.  Accumulators go through an LDS tile [M][256]; for plain stores
+// every thread then takes one column and every (4 / cpw)-th row of it, for
+// the SiLU-gated and argmax epilogues thread t owns column t.  Under split-K
+// each workgroup publishes fp32 partials to scratch [S][M][N]; the last one to
+// arrive on the tile's counter (workspace, zero on entry and on exit)
+// collects them in split order (deterministic), rounds to fp16 and stores or
+// feeds the fused argmax.  4-chunk tiles with plain stores skip the tile: each
+// wave hands off its own chunk.
 
 #pragma once
 #include "lb_common.hpp"
