@@ -452,22 +452,25 @@ def read_traffic(path):
     return None
 
 
-def pmc_probe(torch, lc, dev, calls=24):
-    """Eager headline calls plus a plain elementwise copy of known size, for the
-    FETCH_SIZE / WRITE_SIZE counter runs (the copy calibrates the counters)."""
-    m, k, n = 1, 5120, 17408
-    ns = sets_for(marlin_bytes(m, k, n))
-    prob = MarlinProblem(torch, dev, m, k, n, ns, seed=1)
-    torch.cuda.synchronize()
-    for i in range(calls):
-        prob.call(lc, i % ns)
-    torch.cuda.synchronize()
+def pmc_probe(torch, lc, dev, shapes=((1, 5120, 17408),), calls=24):
+    """Eager calls of each M x K x N shape (the headline by default) plus a
+    plain elementwise copy of known size, for the counter runs (the copy
+    calibrates FETCH_SIZE / WRITE_SIZE)."""
+    for m, k, n in shapes:
+        ns = sets_for(marlin_bytes(m, k, n))
+        prob = MarlinProblem(torch, dev, m, k, n, ns, seed=1)
+        torch.cuda.synchronize()
+        for i in range(calls):
+            prob.call(lc, i % ns)
+        torch.cuda.synchronize()
+        del prob
+        log(f"[pmc-probe] {calls} calls of M={m} K={k} N={n}")
     src = torch.ones((128 * 2 ** 20,), dtype=torch.float16, device=dev)  # 256 MiB read, 256 MiB written
     dst = torch.empty_like(src)
     for _ in range(4):
         torch.add(src, 0, out=dst)
     torch.cuda.synchronize()
-    log(f"[pmc-probe] {calls} headline calls, 4 copies of 256 MiB")
+    log("[pmc-probe] 4 copies of 256 MiB")
 
 
 def gemm_probe(torch, lc, dev, calls=6):
@@ -547,6 +550,8 @@ def main():
     ap.add_argument("--skip-cpu", action="store_true")
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true", help="run the counter-calibration probe and exit")
+    ap.add_argument("--pmc-shapes", default="1x5120x17408",
+                    help="comma-separated MxKxN shapes for --pmc-probe (default: the headline)")
     ap.add_argument("--gemm-probe", action="store_true", help="run the prefill GEMM counter probe and exit")
     ap.add_argument("--mlp-probe", action="store_true", help="time the decode MLP (the reference op pair / lb_marlin_mlp_fused) and exit")
     ap.add_argument("--stream-probe", action="store_true",
@@ -569,7 +574,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.pmc_probe:
-        pmc_probe(torch, lc, dev)
+        pmc_probe(torch, lc, dev, [tuple(int(v) for v in sh.split("x")) for sh in args.pmc_shapes.split(",")])
         return
     if args.gemm_probe:
         gemm_probe(torch, lc, dev)
