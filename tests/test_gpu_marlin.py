@@ -260,6 +260,7 @@ def test_gemm_all_tiles_split_vs_oracle(dev, m, k, n, group):
     (2048, 17408, 5120, 128),  # 320 tiles, 85 of 136 stages per workgroup
     (1000, 1024, 8448, 128),   # ragged last row block; 4.125 stages per workgroup over 8-stage tiles
     (1536, 2048, 8448, -1),    # per-column scales; 12.375 stages per workgroup over 16-stage tiles
+    (2048, 128, 5120, 128),    # one stage per tile: 0 or 1 stage per workgroup, no tile cut
 ])
 def test_gemm_stream_k_vs_oracle(dev, m, k, n, group):
     """The stream-K schedule (128-row tiles filling half to all of one round):
