@@ -185,8 +185,8 @@ __global__ __launch_bounds__(kThreads) void rowwise_fast_kernel(Params p) {
 // sum(x * c) is those sums times 2^(24-off) (exact).  The zero point's share
 // z * sum(x) is staged per unit beside the activations and subtracted once,
 // and the group scale multiplies the unit sum once, as in the fast path.
-// (Scaling the activations by 2^-off instead would flush small ones: fp16
-// arithmetic results below 2^-14 are flushed to zero here.)  Each wave
+// (Scaling the activations by 2^-off instead, for one accumulator, would
+// round those below 2^(off-14) to fp16 subnormals: not exact.)  Each wave
 // computes R rows (of NW matrices) from one LDS read of the activations.
 // ---------------------------------------------------------------------------
 constexpr int kLdsWaves = 8;                       // waves (rows x R) per workgroup, unless the shape below says otherwise
