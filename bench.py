@@ -453,24 +453,42 @@ def read_traffic(path):
 
 
 def pmc_probe(torch, lc, dev, shapes=((1, 5120, 17408),), calls=24):
-    """Eager calls of each M x K x N shape (the headline by default) plus a
-    plain elementwise copy of known size, for the counter runs (the copy
-    calibrates FETCH_SIZE / WRITE_SIZE)."""
-    for m, k, n in shapes:
-        ns = sets_for(marlin_bytes(m, k, n))
-        prob = MarlinProblem(torch, dev, m, k, n, ns, seed=1)
+    """Eager calls of each shape (the headline by default) plus a plain
+    elementwise copy of known size, for the counter runs (the copy calibrates
+    FETCH_SIZE / WRITE_SIZE).  A shape is (M, K, N) for the Marlin GEMV/GEMM or
+    ("rowwise", bits, group, K, N) for the rowwise GEMV."""
+    for sh in shapes:
+        if sh[0] == "rowwise":
+            _, bits, g, k, n = sh
+            ns = sets_for(rowwise_bytes(1, k, n, bits, g))
+            prob = RowwiseProblem(torch, dev, k, n, bits, g, ns, seed=1)
+            what = f"rowwise b{bits} g{g} K={k} N={n}"
+        else:
+            m, k, n = sh
+            ns = sets_for(marlin_bytes(m, k, n))
+            prob = MarlinProblem(torch, dev, m, k, n, ns, seed=1)
+            what = f"M={m} K={k} N={n}"
         torch.cuda.synchronize()
         for i in range(calls):
             prob.call(lc, i % ns)
         torch.cuda.synchronize()
         del prob
-        log(f"[pmc-probe] {calls} calls of M={m} K={k} N={n}")
+        log(f"[pmc-probe] {calls} calls of {what}")
     src = torch.ones((128 * 2 ** 20,), dtype=torch.float16, device=dev)  # 256 MiB read, 256 MiB written
     dst = torch.empty_like(src)
     for _ in range(4):
         torch.add(src, 0, out=dst)
     torch.cuda.synchronize()
     log("[pmc-probe] 4 copies of 256 MiB")
+
+
+def parse_pmc_shape(sh):
+    """'MxKxN' -> (M, K, N); 'rBITSgGROUPxKxN' -> ("rowwise", BITS, GROUP, K, N)."""
+    if sh.startswith("r"):
+        head, k, n = sh[1:].split("x")
+        bits, g = head.split("g")
+        return ("rowwise", int(bits), int(g), int(k), int(n))
+    return tuple(int(v) for v in sh.split("x"))
 
 
 def gemm_probe(torch, lc, dev, calls=6):
@@ -551,7 +569,8 @@ def main():
     ap.add_argument("--skip-extra", action="store_true")
     ap.add_argument("--pmc-probe", action="store_true", help="run the counter-calibration probe and exit")
     ap.add_argument("--pmc-shapes", default="1x5120x17408",
-                    help="comma-separated MxKxN shapes for --pmc-probe (default: the headline)")
+                    help="comma-separated shapes for --pmc-probe: MxKxN (Marlin) or rBITSgGROUPxKxN "
+                         "(rowwise GEMV, e.g. r2g128x17408x5120); default: the headline")
     ap.add_argument("--gemm-probe", action="store_true", help="run the prefill GEMM counter probe and exit")
     ap.add_argument("--mlp-probe", action="store_true", help="time the decode MLP (the reference op pair / lb_marlin_mlp_fused) and exit")
     ap.add_argument("--stream-probe", action="store_true",
@@ -574,7 +593,7 @@ def main():
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     if args.pmc_probe:
-        pmc_probe(torch, lc, dev, [tuple(int(v) for v in sh.split("x")) for sh in args.pmc_shapes.split(",")])
+        pmc_probe(torch, lc, dev, [parse_pmc_shape(sh) for sh in args.pmc_shapes.split(",")])
         return
     if args.gemm_probe:
         gemm_probe(torch, lc, dev)
