@@ -102,10 +102,12 @@ def test_pair_padded_equals_two_singles(dev, bits):
 
 
 @pytest.mark.parametrize("bits", [2, 3, 4, 8])
-@pytest.mark.parametrize("rows,cols,group", [(41, 2048, 128), (7, 5120, 64), (96, 1024, 32)])
+@pytest.mark.parametrize("rows,cols,group", [(41, 2048, 128), (7, 5120, 64), (96, 1024, 32), (19, 17408, 128)])
 def test_pair_whole_units_equals_two_singles(dev, bits, rows, cols, group):
     """Whole 32-code units and one activation row: the pair takes the LDS-staged
-    kernel with both matrices per wave; each output equals its single GEMV."""
+    kernel with both matrices per wave; each output equals its single GEMV.  At
+    2 bits, K = 5120 and 17408 end on a step of 32 units, which runs as half
+    units (one 16-code word per lane)."""
     import torch
     import langburst_cuda as lc
 
