@@ -266,9 +266,8 @@ def test_gemm_stream_k_vs_oracle(dev, m, k, n, group):
     """The stream-K schedule (128-row tiles filling half to all of one round):
     every resident workgroup runs an equal range of the tiles' scale-group
     stages, and tiles cut between workgroups are finished by the last to
-    arrive, summing the parts in k order.  Sampled rows cover every row block
-    and every column; repeated launches are bit-identical; the workspace is
-    left zero."""
+    arrive, summing the parts in k order.  Every output is checked; repeated
+    launches are bit-identical; the workspace is left zero."""
     from neurova_amd import capi
 
     plan = capi.marlin_describe_plan(m, n, k, group)
@@ -276,9 +275,7 @@ def test_gemm_stream_k_vs_oracle(dev, m, k, n, group):
     print_case("gemm-stream-k", m, k, n, group)
     codes, qw, _, sp, x = O.make_marlin_inputs(m, k, n, group, seed=2600 + m + k)
     got = _run_gemm(dev, x, qw, sp, group)
-    rows = np.unique(np.concatenate([np.arange(0, m, 61), [1, 127, 128, 129, m - 2, m - 1]]))
-    rows = rows[rows < m]
-    exact = assert_close_f16(got[rows], O.marlin_gemm(x, qw, sp, group, rows=rows),
+    exact = assert_close_f16(got, O.marlin_gemm(x, qw, sp, group),
                              what=f"gemm-stream-k m={m} k={k} n={n} g={group}")
     assert exact > 0.9
     again = _run_gemm(dev, x, qw, sp, group)
@@ -384,13 +381,14 @@ def test_small_m_gemm_many_splits_vs_oracle(dev, m):
 
 @pytest.mark.parametrize("k,n", [(5120, 17408), (17408, 5120)])
 def test_prefill_shape_cfg3(dev, k, n):
-    """M=2048; a bounded row sample is checked against the oracle."""
+    """M=2048, every output against the oracle (the
+    oracle's dequant dominates its cost; its float64 product of all 2048 rows
+    takes a few seconds)."""
     m = 2048
     print_case("cfg3", m, k, n)
     _, qw, _, sp, x = O.make_marlin_inputs(m, k, n, 128, seed=9)
     got = _run_gemm(dev, x, qw, sp, 128)
-    rows = np.array([0, 1, 15, 16, 127, 128, 1000, 1023, 1024, 2046, 2047])
-    exact = assert_close_f16(got[rows], O.marlin_gemm(x, qw, sp, 128, rows=rows), what=f"cfg3 k={k}")
+    exact = assert_close_f16(got, O.marlin_gemm(x, qw, sp, 128), what=f"cfg3 k={k}")
     assert exact > 0.95
 
 
