@@ -31,9 +31,15 @@ def _inputs(m, k, n, seed, group=128):
 
 
 def _chunks(n, count, seed):
+    """`count` random 64-column chunks plus fixed ones: the first and last two
+    (the mixed plans split the chunks left over after the whole-K tiles, which
+    are the last ones) and both sides of the 256- and 512-chunk boundaries
+    (one and two whole-K tiles per CU on 256 CUs)."""
     rng = np.random.default_rng(seed)
-    picks = np.sort(rng.choice(n // 64, size=min(count, n // 64), replace=False))
-    return [(64 * c, 64 * c + 64) for c in picks]
+    total = n // 64
+    picks = set(rng.choice(total, size=min(count, total), replace=False).tolist())
+    picks |= {c for c in (0, 255, 256, 511, 512, total - 2, total - 1) if 0 <= c < total}
+    return [(64 * c, 64 * c + 64) for c in sorted(picks)]
 
 
 def _oracle_logits(x, qw, s, width=8192):
